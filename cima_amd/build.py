@@ -1,0 +1,75 @@
+"""Build recipe for the native parts of cima_amd (runs on a CPU-only host).
+
+Produces, in ``cima_amd/lib/``:
+  cima_gguf.hsaco     gfx950 code object: every GPU kernel (hipcc --genco)
+  libcima_hip.so      host C ABI (include/cima_hip.h), links libamdhip64
+  libcima_synth.so    seeded synthetic weights + quantisers (include/cima_synth.h)
+
+``python -m cima_amd.build`` rebuilds everything.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+LIB = os.path.join(PKG, "lib")
+INCLUDE = os.path.join(ROOT, "include")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+ARCH = "gfx950"
+
+HSACO = os.path.join(LIB, "cima_gguf.hsaco")
+LIBHIP = os.path.join(LIB, "libcima_hip.so")
+LIBSYNTH = os.path.join(LIB, "libcima_synth.so")
+
+# Device code: gfx950 only.  Packed-FP32 VALU ops are disabled (they have
+# produced silently wrong results on this hardware pool).
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _cmds():
+    hipcc = os.path.join(ROCM, "bin", "hipcc")
+    return {
+        HSACO: [hipcc, *HIPCC_FLAGS, "--genco", "-o", HSACO, os.path.join(CSRC, "gguf_kernels.hip")],
+        LIBHIP: ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                 f"-I{INCLUDE}", f"-I{ROCM}/include", os.path.join(CSRC, "cima_hip.cpp"),
+                 f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-o", LIBHIP],
+        LIBSYNTH: ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-Wall", f"-I{INCLUDE}",
+                   os.path.join(CSRC, "gguf_synth.cpp"), "-o", LIBSYNTH],
+    }
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose: bool = False) -> None:
+    """Compile every native artefact (always recompiles)."""
+    os.makedirs(LIB, exist_ok=True)
+    cmds = _cmds()
+    with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
+        outs = list(ex.map(_run, cmds.values()))
+    if verbose:
+        for o in outs:
+            if o.strip():
+                print(o, file=sys.stderr)
+
+
+def built() -> bool:
+    return all(os.path.exists(p) for p in (HSACO, LIBHIP, LIBSYNTH))
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    print("built:", HSACO, LIBHIP, LIBSYNTH)

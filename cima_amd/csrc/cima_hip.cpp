@@ -1,0 +1,383 @@
+// Host side of the C ABI declared in include/cima_hip.h.
+//
+// The library loads one gfx950 code object (cima_gguf.hsaco, built from
+// gguf_kernels.hip with hipcc --genco) through hipModuleLoad and launches
+// its kernels with hipModuleLaunchKernel -- the HIP counterpart of the
+// reference's CudaCtx (src/cuda.rs), which JIT-compiles kernels.cu with NVRTC
+// and launches through cuLaunchKernel (src/cuda.rs:1112-1151).  No call
+// allocates device memory.
+#include "cima_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <dlfcn.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <unordered_map>
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail((int)e, "hip: %s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+struct Fmt {
+    const char* name;
+    int block_elems;  // elements per block
+    int block_bytes;  // bytes per block
+    int unit_elems;   // elements one lane decodes per step (kernel unit)
+    int w_align;      // required alignment of the weight base pointer
+};
+
+const Fmt* fmt_of(int t) {
+    static const Fmt q8_0 = {"q8_0", 32, 34, 32, 2};
+    static const Fmt q4_0 = {"q4_0", 32, 18, 32, 2};
+    static const Fmt q4_k = {"q4_k", 256, 144, 32, 16};
+    static const Fmt q6_k = {"q6_k", 256, 210, 64, 2};
+    switch (t) {
+    case CIMA_GGML_Q8_0: return &q8_0;
+    case CIMA_GGML_Q4_0: return &q4_0;
+    case CIMA_GGML_Q4_K: return &q4_k;
+    case CIMA_GGML_Q6_K: return &q6_k;
+    default: return nullptr;
+    }
+}
+
+const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_K, CIMA_GGML_Q6_K};
+const int kRows[] = {1, 2, 4, 8};
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int pow2_ceil(int v) {
+    int p = 1;
+    while (p < v) p <<= 1;
+    return p;
+}
+int log2i(int v) {
+    int s = 0;
+    while ((1 << s) < v) s++;
+    return s;
+}
+
+}  // namespace
+
+struct cima_hip_ctx {
+    int device = 0;
+    int num_cu = 0;
+    hipModule_t module = nullptr;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    std::unordered_map<std::string, hipFunction_t> fns;
+    // tuning overrides (0 = heuristic): rows per lane group, lanes per group
+    int tune_rows = 0;
+    int tune_lpr = 0;
+};
+
+namespace {
+
+int get_fn(cima_hip_ctx* ctx, const std::string& name, hipFunction_t* f) {
+    auto it = ctx->fns.find(name);
+    if (it == ctx->fns.end()) return fail(CIMA_E_NO_KERNEL, "kernel %s is not in the code object", name.c_str());
+    *f = it->second;
+    return 0;
+}
+
+int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, void** args, const char* what) {
+    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, ctx->stream, args, nullptr);
+    if (e != hipSuccess) return hip_fail(e, what);
+    return 0;
+}
+
+std::string default_code_object() {
+    Dl_info info;
+    if (dladdr((void*)&cima_hip_init, &info) && info.dli_fname) {
+        std::string p(info.dli_fname);
+        size_t s = p.rfind('/');
+        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) + "/cima_gguf.hsaco";
+    }
+    return "cima_gguf.hsaco";
+}
+
+struct GemvPlan {
+    int rows;       // R: rows per lane group
+    int lpr_shift;  // log2 of lanes per group
+    unsigned grid;  // workgroups of 256 threads
+};
+
+// Lanes per group: enough to cover a row's units in one or two steps (at
+// least 16, at most the whole workgroup).  Rows per group: as many as keep
+// >= 16 waves per CU in flight, so one x fragment serves several rows while
+// every CU still has enough independent loads outstanding to cover HBM
+// latency.  The SwiGLU pair already streams two rows per output row.
+GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pair) {
+    int units = k / F->unit_elems;
+    int lpr = pow2_ceil(units);
+    if (lpr < 16) lpr = 16;
+    if (lpr > 256) lpr = 256;
+    if (ctx->tune_lpr) lpr = ctx->tune_lpr;
+    int groups = 256 / lpr;
+    int rows = pair ? 4 : 8;
+    const long target_waves = (long)ctx->num_cu * 16;
+    while (rows > 1) {
+        long wgs = ((long)n + (long)rows * groups - 1) / ((long)rows * groups);
+        if (wgs * 4 >= target_waves) break;
+        rows >>= 1;
+    }
+    if (ctx->tune_rows) rows = ctx->tune_rows;
+    long wgs = ((long)n + (long)rows * groups - 1) / ((long)rows * groups);
+    return GemvPlan{rows, log2i(lpr), (unsigned)wgs};
+}
+
+int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
+                const void* ba, const void* bb, void* y, int n, int k, int mode, int act, bool pair,
+                const char* api) {
+    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    const Fmt* F = fmt_of(t);
+    if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
+    if (n < 0 || k <= 0 || k % F->block_elems)
+        return fail(CIMA_E_INVALID, "%s: shape n=%d k=%d: k must be a positive multiple of %d for %s", api, n,
+                    k, F->block_elems, F->name);
+    if (act != CIMA_DT_F32 && act != CIMA_DT_F16)
+        return fail(CIMA_E_INVALID, "%s: act_dtype %d is not f32 or f16", api, act);
+    if (!pair && mode != 0 && mode != 1) return fail(CIMA_E_INVALID, "%s: mode %d is not 0, 1 or 2", api, mode);
+    if (n == 0) return 0;
+    if (!x || !wa || !y || (pair && !wb)) return fail(CIMA_E_INVALID, "%s: null x, w or y", api);
+    if (!aligned(x, 16) || !aligned(y, 4) || !aligned(wa, F->w_align) || (pair && !aligned(wb, F->w_align)))
+        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x needs 16 B, %s weights %d B)", api, F->name,
+                    F->w_align);
+    if ((long long)n * (long long)(k / F->block_elems) * F->block_bytes > (1LL << 40))
+        return fail(CIMA_E_INVALID, "%s: weight of %d x %d is beyond the supported size", api, n, k);
+    GemvPlan p = plan_gemv(ctx, F, n, k, pair);
+    char name[96];
+    snprintf(name, sizeof name, "cima_gemv_%s_r%d_%s%s", F->name, p.rows, act == CIMA_DT_F32 ? "f32" : "f16",
+             pair ? "_pair" : "");
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, name, &f)) return rc;
+    const void* xa = x;
+    const void* w0 = wa;
+    const void* w1 = wb;
+    const void* b0 = ba;
+    const void* b1 = bb;
+    void* yy = y;
+    int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
+    void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls};
+    return launch(ctx, f, p.grid, 256, args, api);
+}
+
+}  // namespace
+
+extern "C" {
+
+int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
+    if (!out) return fail(CIMA_E_INVALID, "cima_hip_init: null out pointer");
+    *out = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return fail(CIMA_E_INVALID, "cima_hip_init: device %d out of range (%d devices)", device, count);
+    if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    auto* ctx = new cima_hip_ctx();
+    ctx->device = device;
+    if ((e = hipDeviceGetAttribute(&ctx->num_cu, hipDeviceAttributeMultiprocessorCount, device)) != hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipDeviceGetAttribute(CU count)");
+    }
+    std::string path = code_object ? std::string(code_object) : default_code_object();
+    if ((e = hipModuleLoad(&ctx->module, path.c_str())) != hipSuccess) {
+        delete ctx;
+        return fail((int)e, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
+    }
+    // resolve every kernel up front (the reference's KernelSet)
+    auto add = [&](const std::string& name) -> int {
+        hipFunction_t f;
+        hipError_t r = hipModuleGetFunction(&f, ctx->module, name.c_str());
+        if (r != hipSuccess) return fail((int)r, "hipModuleGetFunction(%s): %s", name.c_str(), hipGetErrorString(r));
+        ctx->fns[name] = f;
+        return 0;
+    };
+    int rc = 0;
+    for (int t : kFormats) {
+        const Fmt* F = fmt_of(t);
+        for (int r : kRows)
+            for (const char* act : {"f32", "f16"})
+                for (const char* sfx : {"", "_pair"}) {
+                    char name[96];
+                    snprintf(name, sizeof name, "cima_gemv_%s_r%d_%s%s", F->name, r, act, sfx);
+                    if (!rc) rc = add(name);
+                }
+        if (!rc) rc = add(std::string("cima_dequant_") + F->name);
+        if (!rc) rc = add(std::string("cima_gather_") + F->name);
+    }
+    if (rc) {
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return rc;
+    }
+    if ((e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking)) != hipSuccess) {
+        (void)hipModuleUnload(ctx->module);
+        delete ctx;
+        return hip_fail(e, "hipStreamCreateWithFlags");
+    }
+    ctx->stream = ctx->own_stream;
+    int er = 0, el = 0;
+    if (const char* s = getenv("CIMA_GEMV_ROWS")) er = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_LPR")) el = atoi(s);
+    if (er || el) {
+        if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
+            cima_hip_destroy(ctx);
+            return r;
+        }
+    }
+    *out = ctx;
+    return 0;
+}
+
+int cima_hip_destroy(cima_hip_ctx* ctx) {
+    if (!ctx) return 0;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->own_stream) {
+        (void)hipStreamSynchronize(ctx->own_stream);
+        (void)hipStreamDestroy(ctx->own_stream);
+    }
+    if (ctx->module) (void)hipModuleUnload(ctx->module);
+    ctx->module = nullptr;
+    delete ctx;
+    return 0;
+}
+
+int cima_hip_bind(cima_hip_ctx* ctx) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_bind: null context");
+    hipError_t e = hipSetDevice(ctx->device);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipSetDevice");
+}
+
+int cima_hip_set_stream(cima_hip_ctx* ctx, void* s) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_stream: null context");
+    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    return 0;
+}
+
+void* cima_hip_get_stream(cima_hip_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int cima_hip_sync(cima_hip_ctx* ctx) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_sync: null context");
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipStreamSynchronize");
+}
+
+const char* cima_hip_last_error(void) { return g_err; }
+
+int cima_hip_is_fatal(int code) {
+    // Sticky codes after which the device context cannot be used; the same
+    // numeric set as the reference's cu_fatal (src/cuda.rs:122-127) --
+    // hipError_t keeps CUDA's numbering for these (700 illegal address,
+    // 702 launch timeout, 710 device assert, 719 launch failure, ...).
+    // 701 (launch out of resources) is not sticky.
+    switch (code) {
+    case 700: case 702: case 710: case 713: case 714: case 715:
+    case 716: case 717: case 718: case 719:
+        return 1;
+    default:
+        return 0;
+    }
+}
+
+int cima_hip_num_cu(cima_hip_ctx* ctx) { return ctx ? ctx->num_cu : 0; }
+
+int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lpr) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_tuning: null context");
+    if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 8)
+        return fail(CIMA_E_INVALID, "cima_hip_set_gemv_tuning: rows %d is not 0, 1, 2, 4 or 8", rows);
+    if (lpr != 0 && (lpr < 16 || lpr > 256 || (lpr & (lpr - 1))))
+        return fail(CIMA_E_INVALID, "cima_hip_set_gemv_tuning: lanes %d is not 0 or a power of two in [16, 256]", lpr);
+    ctx->tune_rows = rows;
+    ctx->tune_lpr = lpr;
+    return 0;
+}
+
+int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int t, const void* x, const void* w, const void* bias, void* y, int n,
+                       int k, int mode, int act) {
+    if (mode == 2) {
+        // gate|up pair stored as one [2n, k] weight; bias has 2n entries
+        const Fmt* F = fmt_of(t);
+        if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_gemv: ggml type %d is not a supported GGUF block format", t);
+        if (k <= 0 || k % F->block_elems)
+            return fail(CIMA_E_INVALID, "cima_hip_gguf_gemv: k=%d must be a positive multiple of %d", k,
+                        F->block_elems);
+        size_t row_bytes = (size_t)(k / F->block_elems) * F->block_bytes;
+        size_t esz = act == CIMA_DT_F32 ? 4 : 2;
+        const char* wu = w ? (const char*)w + (size_t)(n > 0 ? n : 0) * row_bytes : nullptr;
+        const char* bu = bias ? (const char*)bias + (size_t)(n > 0 ? n : 0) * esz : nullptr;
+        return gemv_common(ctx, t, x, w, wu, bias, bu, y, n, k, 2, act, true, "cima_hip_gguf_gemv");
+    }
+    return gemv_common(ctx, t, x, w, nullptr, bias, nullptr, y, n, k, mode, act, false, "cima_hip_gguf_gemv");
+}
+
+int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int t, const void* x, const void* wg, const void* wu,
+                              const void* bg, const void* bu, void* y, int n, int k, int act) {
+    return gemv_common(ctx, t, x, wg, wu, bg, bu, y, n, k, 2, act, true, "cima_hip_gguf_gemv_swiglu");
+}
+
+int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int t, const void* src, void* out, long long nblocks) {
+    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_dequant: context is not initialised");
+    const Fmt* F = fmt_of(t);
+    if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_dequant: ggml type %d is not a supported GGUF block format", t);
+    if (nblocks < 0) return fail(CIMA_E_INVALID, "cima_hip_gguf_dequant: nblocks %lld < 0", nblocks);
+    if (nblocks == 0) return 0;
+    if (!src || !out) return fail(CIMA_E_INVALID, "cima_hip_gguf_dequant: null pointer");
+    if (!aligned(src, F->w_align) || !aligned(out, 16))
+        return fail(CIMA_E_INVALID, "cima_hip_gguf_dequant: misaligned src (%d B) or out (16 B)", F->w_align);
+    long long units = nblocks * (F->block_elems / F->unit_elems);
+    long long grid = (units + 255) / 256;
+    if (grid > 0x7fffffffLL) return fail(CIMA_E_INVALID, "cima_hip_gguf_dequant: %lld blocks is too many", nblocks);
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, std::string("cima_dequant_") + F->name, &f)) return rc;
+    const void* s = src;
+    void* o = out;
+    long long nb = nblocks;
+    void* args[] = {&s, &o, &nb};
+    return launch(ctx, f, (unsigned)grid, 256, args, "cima_hip_gguf_dequant");
+}
+
+int cima_hip_gguf_gather(cima_hip_ctx* ctx, int t, const void* table, const unsigned int* ids, void* out, int n,
+                         int hidden) {
+    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_gather: context is not initialised");
+    const Fmt* F = fmt_of(t);
+    if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_gather: ggml type %d is not a supported GGUF block format", t);
+    if (n < 0 || hidden <= 0 || hidden % F->block_elems)
+        return fail(CIMA_E_INVALID, "cima_hip_gguf_gather: n=%d hidden=%d (hidden must be a multiple of %d)", n,
+                    hidden, F->block_elems);
+    if (n == 0) return 0;
+    if (!table || !ids || !out) return fail(CIMA_E_INVALID, "cima_hip_gguf_gather: null pointer");
+    if (!aligned(table, F->w_align) || !aligned(out, 16))
+        return fail(CIMA_E_INVALID, "cima_hip_gguf_gather: misaligned table (%d B) or out (16 B)", F->w_align);
+    long long units = (long long)n * (hidden / F->unit_elems);
+    long long grid = (units + 255) / 256;
+    if (grid > 0x7fffffffLL) return fail(CIMA_E_INVALID, "cima_hip_gguf_gather: too many rows");
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, std::string("cima_gather_") + F->name, &f)) return rc;
+    const void* tb = table;
+    const void* id = ids;
+    void* o = out;
+    int nn = n, hh = hidden;
+    void* args[] = {&tb, &id, &o, &nn, &hh};
+    return launch(ctx, f, (unsigned)grid, 256, args, "cima_hip_gguf_gather");
+}
+
+}  // extern "C"

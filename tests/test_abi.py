@@ -1,0 +1,119 @@
+"""CPU tests of the product's host side: the C ABI exports, format tables,
+the synthetic quantisers (decoded by the oracle), and loud failure without
+a GPU."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+import oracle
+from cima_amd import gguf, synth
+from cima_amd import hip as hipmod
+from cima_amd import build as cbuild
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FORMATS = [gguf.DType.Q8_0, gguf.DType.Q4_0, gguf.DType.Q4_K, gguf.DType.Q6_K]
+
+
+def header_functions(path):
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(cima_\w+)\s*\(", text)
+
+
+@pytest.mark.parametrize("header,lib", [("cima_hip.h", cbuild.LIBHIP), ("cima_synth.h", cbuild.LIBSYNTH)])
+def test_library_exports_every_declared_symbol(header, lib):
+    names = header_functions(os.path.join(ROOT, "include", header))
+    assert names, header
+    L = ctypes.CDLL(lib)
+    for n in names:
+        assert hasattr(L, n), f"{os.path.basename(lib)} does not export {n}"
+
+
+def test_python_binding_covers_header():
+    names = header_functions(os.path.join(ROOT, "include", "cima_hip.h"))
+    assert set(names) == set(hipmod.EXPORTS)
+
+
+def test_code_object_holds_every_kernel():
+    blob = open(cbuild.HSACO, "rb").read()
+    assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    for f in ("q8_0", "q4_0", "q4_k", "q6_k"):
+        for r in (1, 2, 4, 8):
+            for a in ("f32", "f16"):
+                for sfx in ("", "_pair"):
+                    assert f"cima_gemv_{f}_r{r}_{a}{sfx}".encode() in blob
+        assert f"cima_dequant_{f}".encode() in blob
+        assert f"cima_gather_{f}".encode() in blob
+    assert b"gfx950" in blob
+
+
+def test_error_classification():
+    L = hipmod.load_library()
+    for c in (700, 702, 710, 713, 719):
+        assert L.cima_hip_is_fatal(c) == 1
+    for c in (0, 1, 2, 701, 98, -1):
+        assert L.cima_hip_is_fatal(c) == 0
+
+
+def test_null_context_is_rejected():
+    L = hipmod.load_library()
+    rc = L.cima_hip_gguf_gemv(None, 12, None, None, None, None, 1, 256, 0, 0)
+    assert rc == hipmod.E_NOT_INIT
+    assert b"not initialised" in L.cima_hip_last_error()
+    assert L.cima_hip_gguf_dequant(None, 12, None, None, 1) == hipmod.E_NOT_INIT
+    assert L.cima_hip_sync(None) == hipmod.E_NOT_INIT
+
+
+def test_hipctx_fails_loudly_without_device():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    with pytest.raises(hipmod.EngineError):
+        hipmod.HipCtx(0)
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=lambda t: t.name)
+def test_format_tables_match_oracle(t):
+    assert gguf.block_elems(t) == oracle.BLOCK_ELEMS[t]
+    assert t.block_bytes == oracle.BLOCK_BYTES[t]
+    for numel in (0, 256, 4096, 14336 * 4096):
+        assert gguf.storage_bytes(t, numel) == oracle.storage_bytes(t, numel)
+    with pytest.raises(ValueError):
+        gguf.storage_bytes(13, 256)
+
+
+def test_synth_normal_is_deterministic_and_normal():
+    a = synth.normal(42, 0.02, 1 << 20, threads=4)
+    b = synth.normal(42, 0.02, 1 << 20, threads=1)
+    assert np.array_equal(a, b)
+    assert abs(a.mean()) < 1e-4 and abs(a.std() - 0.02) < 2e-4
+    c = synth.normal(43, 0.02, 1 << 10)
+    assert not np.array_equal(a[:1024], c)
+
+
+# relative normwise quantisation error bounds of the synthetic quantisers
+QERR = {gguf.DType.Q8_0: 0.01, gguf.DType.Q4_0: 0.2, gguf.DType.Q4_K: 0.12, gguf.DType.Q6_K: 0.04}
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=lambda t: t.name)
+def test_synth_quantisers_roundtrip_through_oracle(t):
+    rows, k = 64, 1024
+    w = synth.normal(7, 0.02, rows * k).reshape(rows, k)
+    packed = synth.quantize(t, w)
+    assert packed.shape == (rows, gguf.row_bytes(t, k))
+    deq = oracle.f16_bits_to_f32(oracle.dequant(t, packed.reshape(-1), rows * k)).reshape(rows, k)
+    err = np.linalg.norm(deq - w) / np.linalg.norm(w)
+    assert err < QERR[t], err
+    # weights() is normal() + quantize() without the fp32 matrix
+    assert np.array_equal(synth.weights(t, 7, 0.02, rows, k), packed)
+
+
+def test_synth_rejects_bad_shapes():
+    with pytest.raises(ValueError):
+        synth.quantize(12, np.zeros((2, 100), np.float32))
+    with pytest.raises(ValueError):
+        synth.weights(13, 1, 0.02, 2, 256)
