@@ -27,9 +27,12 @@ LIBHIP = os.path.join(LIB, "libcima_hip.so")
 LIBSYNTH = os.path.join(LIB, "libcima_synth.so")
 
 # Device code: gfx950 only.  Packed-FP32 VALU ops are disabled (they have
-# produced silently wrong results on this hardware pool).
+# produced silently wrong results on this hardware pool).  No implicit FP
+# contraction: the dequantisers must round exactly like the host decoders
+# (a fused f32->f16 multiply would drop the sign of -0 and the intermediate
+# f32 rounding of Q4_K); the GEMV code asks for its FMAs explicitly.
 HIPCC_FLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 

@@ -40,15 +40,17 @@ struct Fmt {
     const char* name;
     int block_elems;  // elements per block
     int block_bytes;  // bytes per block
-    int unit_elems;   // elements one lane decodes per step (kernel unit)
+    int unit_elems;   // elements one lane decodes per dequant/gather step
     int w_align;      // required alignment of the weight base pointer
+    int gemv_unit;    // elements one lane decodes per GEMV step
+    int pad_shift;    // GEMV x staging: 16 B of LDS padding per 2^pad_shift elements
 };
 
 const Fmt* fmt_of(int t) {
-    static const Fmt q8_0 = {"q8_0", 32, 34, 32, 2};
-    static const Fmt q4_0 = {"q4_0", 32, 18, 32, 2};
-    static const Fmt q4_k = {"q4_k", 256, 144, 32, 16};
-    static const Fmt q6_k = {"q6_k", 256, 210, 64, 2};
+    static const Fmt q8_0 = {"q8_0", 32, 34, 32, 2, 32, 5};
+    static const Fmt q4_0 = {"q4_0", 32, 18, 32, 2, 32, 5};
+    static const Fmt q4_k = {"q4_k", 256, 144, 32, 16, 64, 6};
+    static const Fmt q6_k = {"q6_k", 256, 210, 64, 2, 64, 6};
     switch (t) {
     case CIMA_GGML_Q8_0: return &q8_0;
     case CIMA_GGML_Q4_0: return &q4_0;
@@ -59,7 +61,8 @@ const Fmt* fmt_of(int t) {
 }
 
 const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_K, CIMA_GGML_Q6_K};
-const int kRows[] = {1, 2, 4, 8};
+// (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
+const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
@@ -79,6 +82,7 @@ int log2i(int v) {
 struct cima_hip_ctx {
     int device = 0;
     int num_cu = 0;
+    int max_lds = 0;  // bytes of LDS one workgroup may use
     hipModule_t module = nullptr;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
@@ -86,6 +90,7 @@ struct cima_hip_ctx {
     // tuning overrides (0 = heuristic): rows per lane group, lanes per group
     int tune_rows = 0;
     int tune_lpr = 0;
+    int tune_wgs = 0;  // workgroups per CU of the persistent grid (0 = built-in default)
 };
 
 namespace {
@@ -97,8 +102,9 @@ int get_fn(cima_hip_ctx* ctx, const std::string& name, hipFunction_t* f) {
     return 0;
 }
 
-int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, void** args, const char* what) {
-    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, 0, ctx->stream, args, nullptr);
+int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, void** args, const char* what,
+           unsigned lds = 0) {
+    hipError_t e = hipModuleLaunchKernel(f, grid, 1, 1, block, 1, 1, lds, ctx->stream, args, nullptr);
     if (e != hipSuccess) return hip_fail(e, what);
     return 0;
 }
@@ -114,33 +120,46 @@ std::string default_code_object() {
 }
 
 struct GemvPlan {
-    int rows;       // R: rows per lane group
-    int lpr_shift;  // log2 of lanes per group
-    unsigned grid;  // workgroups of 256 threads
+    int rows;        // R: rows per lane group
+    int iters;       // unit steps per row and lane
+    int lpr_shift;   // log2 of lanes per group (16..64, inside one wave)
+    unsigned grid;   // workgroups of 256 threads
+    unsigned lds;    // dynamic LDS bytes: x as two int8 planes + padding, scales, sums
 };
 
-// Lanes per group: enough to cover a row's units in one or two steps (at
-// least 16, at most the whole workgroup).  Rows per group: as many as keep
-// >= 16 waves per CU in flight, so one x fragment serves several rows while
-// every CU still has enough independent loads outstanding to cover HBM
-// latency.  The SwiGLU pair already streams two rows per output row.
+// matches xstage_bytes() in gguf_kernels.hip
+size_t gemv_lds_bytes(const Fmt* F, int k) {
+    size_t kk = (size_t)k;
+    return 2 * kk + 16 * (kk >> F->pad_shift) + 4 * (kk >> 5) + 4 * (kk >> 4);
+}
+
+bool have_shape(int r, int it) {
+    for (const auto& sh : kShapes)
+        if (sh[0] == r && sh[1] == it) return true;
+    return false;
+}
+
+// Lanes per group: a power of two in [16, 64] such that a row takes at most
+// 8 unit steps; rows per group: as many as the built shapes allow (up to 4,
+// 2 for the SwiGLU pair, which streams two weights per output row) while
+// every CU still gets >= 8 groups.  The grid covers every row group once
+// with groups dealt out evenly, capped at what fits on the device at once.
 GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pair) {
-    int units = k / F->unit_elems;
+    int units = k / F->gemv_unit;
     int lpr = pow2_ceil(units);
     if (lpr < 16) lpr = 16;
-    if (lpr > 256) lpr = 256;
-    if (ctx->tune_lpr) lpr = ctx->tune_lpr;
-    int groups = 256 / lpr;
-    int rows = pair ? 4 : 8;
-    const long target_waves = (long)ctx->num_cu * 16;
-    while (rows > 1) {
-        long wgs = ((long)n + (long)rows * groups - 1) / ((long)rows * groups);
-        if (wgs * 4 >= target_waves) break;
-        rows >>= 1;
-    }
-    if (ctx->tune_rows) rows = ctx->tune_rows;
-    long wgs = ((long)n + (long)rows * groups - 1) / ((long)rows * groups);
-    return GemvPlan{rows, log2i(lpr), (unsigned)wgs};
+    if (lpr > 64) lpr = 64;
+    if (ctx->tune_lpr) lpr = ctx->tune_lpr > 64 ? 64 : ctx->tune_lpr;
+    int iters = (units + lpr - 1) / lpr;
+    int it = 1;
+    while (it < iters) it <<= 1;
+    int rows = 1;  // measured fastest for every decode shape; 2 is kept for tuning
+    (void)pair;
+    if (ctx->tune_rows && have_shape(ctx->tune_rows, it)) rows = ctx->tune_rows;
+    long groups_per_wg = 4L * (64 / lpr);
+    long row_groups = ((long)n + rows - 1) / rows;
+    long wgs = (row_groups + groups_per_wg - 1) / groups_per_wg;
+    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k)};
 }
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
@@ -163,11 +182,27 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if ((long long)n * (long long)(k / F->block_elems) * F->block_bytes > (1LL << 40))
         return fail(CIMA_E_INVALID, "%s: weight of %d x %d is beyond the supported size", api, n, k);
     GemvPlan p = plan_gemv(ctx, F, n, k, pair);
+    if ((long)p.lds > ctx->max_lds)
+        return fail(CIMA_E_INVALID, "%s: k=%d needs %u B of LDS for x, the device allows %d", api, k, p.lds,
+                    ctx->max_lds);
     char name[96];
-    snprintf(name, sizeof name, "cima_gemv_%s_r%d_%s%s", F->name, p.rows, act == CIMA_DT_F32 ? "f32" : "f16",
-             pair ? "_pair" : "");
+    if (p.iters > 8)
+        return fail(CIMA_E_INVALID, "%s: k=%d is longer than the GEMV supports (%d units per lane group)", api, k,
+                    p.iters);
+    const bool epi = ba != nullptr || bb != nullptr || mode == 1;
+    snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s", F->name, p.rows, p.iters,
+             act == CIMA_DT_F32 ? "f32" : "f16", pair ? "_pair" : "", epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
+    int resident = 0;
+    hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, 256, p.lds);
+    if (oe != hipSuccess) return hip_fail(oe, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (resident < 1) resident = 1;
+    // two workgroups per CU measured best for every decode shape on MI355X
+    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : 2;
+    if (want < resident) resident = want;
+    unsigned cap = (unsigned)(resident * ctx->num_cu);
+    if (p.grid > cap) p.grid = cap;
     const void* xa = x;
     const void* w0 = wa;
     const void* w1 = wb;
@@ -176,7 +211,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     void* yy = y;
     int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
     void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls};
-    return launch(ctx, f, p.grid, 256, args, api);
+    return launch(ctx, f, p.grid, 256, args, api, p.lds);
 }
 
 }  // namespace
@@ -198,6 +233,11 @@ int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
         delete ctx;
         return hip_fail(e, "hipDeviceGetAttribute(CU count)");
     }
+    if ((e = hipDeviceGetAttribute(&ctx->max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, device)) !=
+        hipSuccess) {
+        delete ctx;
+        return hip_fail(e, "hipDeviceGetAttribute(LDS per block)");
+    }
     std::string path = code_object ? std::string(code_object) : default_code_object();
     if ((e = hipModuleLoad(&ctx->module, path.c_str())) != hipSuccess) {
         delete ctx;
@@ -214,11 +254,11 @@ int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
     int rc = 0;
     for (int t : kFormats) {
         const Fmt* F = fmt_of(t);
-        for (int r : kRows)
+        for (const auto& sh : kShapes)
             for (const char* act : {"f32", "f16"})
-                for (const char* sfx : {"", "_pair"}) {
+                for (const char* sfx : {"", "_epi", "_pair", "_pair_epi"}) {
                     char name[96];
-                    snprintf(name, sizeof name, "cima_gemv_%s_r%d_%s%s", F->name, r, act, sfx);
+                    snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
                     if (!rc) rc = add(name);
                 }
         if (!rc) rc = add(std::string("cima_dequant_") + F->name);
@@ -238,6 +278,7 @@ int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
     int er = 0, el = 0;
     if (const char* s = getenv("CIMA_GEMV_ROWS")) er = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_LPR")) el = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -300,10 +341,18 @@ int cima_hip_is_fatal(int code) {
 
 int cima_hip_num_cu(cima_hip_ctx* ctx) { return ctx ? ctx->num_cu : 0; }
 
+int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_grid: null context");
+    if (wgs_per_cu < 0 || wgs_per_cu > 64)
+        return fail(CIMA_E_INVALID, "cima_hip_set_gemv_grid: %d workgroups per CU is out of range", wgs_per_cu);
+    ctx->tune_wgs = wgs_per_cu;
+    return 0;
+}
+
 int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lpr) {
     if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_tuning: null context");
-    if (rows != 0 && rows != 1 && rows != 2 && rows != 4 && rows != 8)
-        return fail(CIMA_E_INVALID, "cima_hip_set_gemv_tuning: rows %d is not 0, 1, 2, 4 or 8", rows);
+    if (rows != 0 && rows != 1 && rows != 2)
+        return fail(CIMA_E_INVALID, "cima_hip_set_gemv_tuning: rows %d is not 0, 1 or 2", rows);
     if (lpr != 0 && (lpr < 16 || lpr > 256 || (lpr & (lpr - 1))))
         return fail(CIMA_E_INVALID, "cima_hip_set_gemv_tuning: lanes %d is not 0 or a power of two in [16, 256]", lpr);
     ctx->tune_rows = rows;

@@ -30,6 +30,7 @@ HSACO = os.path.join(LIB_DIR, "cima_gguf.hsaco")
 EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
+    "cima_hip_set_gemv_grid",
     "cima_hip_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
 )
@@ -69,6 +70,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_is_fatal.argtypes = [I]
     L.cima_hip_num_cu.argtypes = [P]
     L.cima_hip_set_gemv_tuning.argtypes = [P, I, I]
+    L.cima_hip_set_gemv_grid.argtypes = [P, I]
     L.cima_hip_gguf_gemv.argtypes = [P, I, P, P, P, P, I, I, I, I]
     L.cima_hip_gguf_gemv_swiglu.argtypes = [P, I, P, P, P, P, P, P, I, I, I]
     L.cima_hip_gguf_dequant.argtypes = [P, I, P, P, LL]
@@ -155,6 +157,10 @@ class HipCtx:
     def set_gemv_tuning(self, rows: int = 0, lanes_per_row: int = 0) -> None:
         """Override the GEMV launch plan (0, 0 = built-in heuristic)."""
         self._check(self.lib.cima_hip_set_gemv_tuning(self.handle, rows, lanes_per_row))
+
+    def set_gemv_grid(self, wgs_per_cu: int = 0) -> None:
+        """Cap the persistent GEMV grid at this many workgroups per CU (0 = fill)."""
+        self._check(self.lib.cima_hip_set_gemv_grid(self.handle, wgs_per_cu))
 
     # -- the GGUF hot path --------------------------------------------------
     def gguf_gemv(self, fmt: int, x, w, bias, y, n: int, k: int, mode: int = 0,

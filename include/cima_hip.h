@@ -79,11 +79,16 @@ int cima_hip_is_fatal(int code);
 int cima_hip_num_cu(cima_hip_ctx* ctx);
 
 /* GEMV launch tuning (no counterpart in the reference): rows per lane group
- * (1, 2, 4 or 8) and lanes per group (16..256, a power of two) for every
+ * (1 or 2) and lanes per group (16..256, a power of two) for every
  * later gguf_gemv call on this context; 0 restores the built-in heuristic.
  * The environment variables CIMA_GEMV_ROWS / CIMA_GEMV_LPR set the initial
  * values at cima_hip_init. */
 int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
+
+/* GEMV grid tuning (no counterpart in the reference): the persistent grid
+ * holds at most this many workgroups per CU (0 = the default of 2, or fewer
+ * if fewer fit; environment variable CIMA_GEMV_WGS at init). */
+int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
 /* Fused dequant-GEMV: replaces CudaCtx::gguf_gemv (src/cuda.rs:2161-2220).
  *   y[r] = sum_j W[r, j] * x[j] for r in [0, n), W packed GGUF rows of k

@@ -54,6 +54,12 @@ def _round(v64: np.ndarray) -> np.ndarray:
 
 def decode(t: int, src: np.ndarray) -> np.ndarray:
     """Packed blocks -> f16 bits, one row of elements per block, flattened."""
+    return _round(decode_exact(t, src))
+
+
+def decode_exact(t: int, src: np.ndarray) -> np.ndarray:
+    """Packed blocks -> the exact real value of every element (float64, no
+    rounding at all), flattened."""
     be, bb = BLOCK[t]
     b = np.asarray(src, dtype=np.uint8).reshape(-1, bb)
     nb = b.shape[0]
@@ -99,7 +105,7 @@ def decode(t: int, src: np.ndarray) -> np.ndarray:
             v = v.reshape(nb, 256)
         else:
             raise ValueError(t)
-    return _round(v).reshape(-1)
+    return v.reshape(-1)
 
 
 def sane_scales(t: int, blocks: np.ndarray) -> np.ndarray:

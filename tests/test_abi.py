@@ -41,10 +41,10 @@ def test_code_object_holds_every_kernel():
     blob = open(cbuild.HSACO, "rb").read()
     assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
     for f in ("q8_0", "q4_0", "q4_k", "q6_k"):
-        for r in (1, 2, 4, 8):
+        for r, it in ((1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4)):
             for a in ("f32", "f16"):
-                for sfx in ("", "_pair"):
-                    assert f"cima_gemv_{f}_r{r}_{a}{sfx}".encode() in blob
+                for sfx in ("", "_epi", "_pair", "_pair_epi"):
+                    assert f"cima_gemv_{f}_r{r}_i{it}_{a}{sfx}".encode() in blob
         assert f"cima_dequant_{f}".encode() in blob
         assert f"cima_gather_{f}".encode() in blob
     assert b"gfx950" in blob
