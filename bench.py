@@ -163,6 +163,7 @@ def main():
         return best
 
     per_shape = {}
+    gemm_flops = {}
     # the roofline kernel: fused gate+up SwiGLU, cold over the 32 layers
     pair_bytes = 2 * wbytes(Q4_K, FFN, HID) + 4 * HID + 4 * FFN
     pair_us = time_calls(lambda L: ctx.gguf_gemv_swiglu(Q4_K, h, L["gate"], L["up"], None, None, act, FFN, HID),
@@ -184,11 +185,24 @@ def main():
             shape_leg(nm, Q4_K, n, k)
         shape_leg("q8_0 4864x896 (config 1)", Q8_0, 4864, 896)
         shape_leg("q6_k 128256x4096 (config 3 head)", Q6_K, 128256, HID, copies_mb=900)
+        # config 4: prefill dequant-GEMM on MFMA, Q4_K 14336x4096, X bf16 (m tokens), Y fp32
+        gw = synth.weights(Q4_K, 300, 0.02, FFN, HID)
+        gbufs = [torch.from_numpy(gw).to(dev) for _ in range(12)]
+        for m in (16, 128, 512):
+            gx = torch.from_numpy(synth.normal(301, 1.0, m * HID)).to(dev).to(torch.bfloat16).reshape(m, HID)
+            gy = torch.empty((m, FFN), device=dev)
+            us = time_calls(lambda b: ctx.gguf_gemm(Q4_K, gx, b, gy, m, FFN, HID), gbufs, calls=24)
+            b = wbytes(Q4_K, FFN, HID) + 2 * m * HID + 4 * m * FFN
+            per_shape[f"q4_k gemm 14336x4096 m={m} (config 4)"] = (us, b)
+            gemm_flops[f"q4_k gemm 14336x4096 m={m} (config 4)"] = 2.0 * FFN * HID * m
 
     shapes_out = {}
     for name, (us, b) in per_shape.items():
         shapes_out[name] = {"us_per_call": round(us, 3), "gb_s": round(b / us / 1e3, 1),
                             "hbm_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": b}
+        if name in gemm_flops:
+            tf = gemm_flops[name] / us / 1e6
+            shapes_out[name].update({"tflop_s": round(tf, 1), "mfma_frac_f16_dense": round(tf / 2500.0, 4)})
 
     achieved = pair_bytes / pair_us / 1e3
     traffic = None

@@ -1,7 +1,9 @@
 """Build recipe for the native parts of cima_amd (runs on a CPU-only host).
 
 Produces, in ``cima_amd/lib/``:
-  cima_gguf.hsaco     gfx950 code object: every GPU kernel (hipcc --genco)
+  cima_gemv.hsaco     gfx950 code objects (hipcc --genco): decode GEMVs,
+  cima_gemm.hsaco       prefill dequant-GEMMs (MFMA),
+  cima_dequant.hsaco    dequant-to-f16 and packed gather
   libcima_hip.so      host C ABI (include/cima_hip.h), links libamdhip64
   libcima_synth.so    seeded synthetic weights + quantisers (include/cima_synth.h)
 
@@ -22,7 +24,7 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HSACO = os.path.join(LIB, "cima_gguf.hsaco")
+HSACOS = {name: os.path.join(LIB, f"cima_{name}.hsaco") for name in ("gemv", "gemm", "dequant")}
 LIBHIP = os.path.join(LIB, "libcima_hip.so")
 LIBSYNTH = os.path.join(LIB, "libcima_synth.so")
 
@@ -40,7 +42,8 @@ HIPCC_FLAGS = [
 def _cmds():
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     return {
-        HSACO: [hipcc, *HIPCC_FLAGS, "--genco", "-o", HSACO, os.path.join(CSRC, "gguf_kernels.hip")],
+        **{path: [hipcc, *HIPCC_FLAGS, f"-I{CSRC}", "--genco", "-o", path, os.path.join(CSRC, f"gguf_{name}.hip")]
+           for name, path in HSACOS.items()},
         LIBHIP: ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
                  f"-I{INCLUDE}", f"-I{ROCM}/include", os.path.join(CSRC, "cima_hip.cpp"),
                  f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-ldl", "-o", LIBHIP],
@@ -70,9 +73,9 @@ def build(verbose: bool = False) -> None:
 
 
 def built() -> bool:
-    return all(os.path.exists(p) for p in (HSACO, LIBHIP, LIBSYNTH))
+    return all(os.path.exists(p) for p in (*HSACOS.values(), LIBHIP, LIBSYNTH))
 
 
 if __name__ == "__main__":
     build(verbose=True)
-    print("built:", HSACO, LIBHIP, LIBSYNTH)
+    print("built:", *HSACOS.values(), LIBHIP, LIBSYNTH)

@@ -1,11 +1,11 @@
 // Host side of the C ABI declared in include/cima_hip.h.
 //
-// The library loads one gfx950 code object (cima_gguf.hsaco, built from
-// gguf_kernels.hip with hipcc --genco) through hipModuleLoad and launches
-// its kernels with hipModuleLaunchKernel -- the HIP counterpart of the
-// reference's CudaCtx (src/cuda.rs), which JIT-compiles kernels.cu with NVRTC
-// and launches through cuLaunchKernel (src/cuda.rs:1112-1151).  No call
-// allocates device memory.
+// The library loads three gfx950 code objects (cima_gemv / cima_gemm /
+// cima_dequant .hsaco, built from gguf_*.hip with hipcc --genco) through
+// hipModuleLoad and launches their kernels with hipModuleLaunchKernel -- the
+// HIP counterpart of the reference's CudaCtx (src/cuda.rs), which
+// JIT-compiles kernels.cu with NVRTC and launches through cuLaunchKernel
+// (src/cuda.rs:1112-1151).  No call allocates device memory.
 #include "cima_hip.h"
 
 #include <hip/hip_runtime.h>
@@ -61,6 +61,9 @@ const Fmt* fmt_of(int t) {
 }
 
 const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_K, CIMA_GGML_Q6_K};
+// prefill GEMM token-tile widths the code object is built for
+const int kGemmBN[] = {16, 64, 128};
+
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
 
@@ -83,7 +86,8 @@ struct cima_hip_ctx {
     int device = 0;
     int num_cu = 0;
     int max_lds = 0;  // bytes of LDS one workgroup may use
-    hipModule_t module = nullptr;
+    hipModule_t modules[3] = {nullptr, nullptr, nullptr};  // gemv, gemm, dequant
+    bool loaded = false;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns;
@@ -91,6 +95,7 @@ struct cima_hip_ctx {
     int tune_rows = 0;
     int tune_lpr = 0;
     int tune_wgs = 0;  // workgroups per CU of the persistent grid (0 = built-in default)
+    int tune_gemm_bn = 0;  // prefill GEMM token tile (0 = smallest built one covering m)
 };
 
 namespace {
@@ -109,14 +114,24 @@ int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, vo
     return 0;
 }
 
-std::string default_code_object() {
+const char* const kModuleFiles[3] = {"cima_gemv.hsaco", "cima_gemm.hsaco", "cima_dequant.hsaco"};
+
+std::string default_code_dir() {
     Dl_info info;
     if (dladdr((void*)&cima_hip_init, &info) && info.dli_fname) {
         std::string p(info.dli_fname);
         size_t s = p.rfind('/');
-        return (s == std::string::npos ? std::string(".") : p.substr(0, s)) + "/cima_gguf.hsaco";
+        return s == std::string::npos ? std::string(".") : p.substr(0, s);
     }
-    return "cima_gguf.hsaco";
+    return ".";
+}
+
+void unload(cima_hip_ctx* ctx) {
+    for (auto& m : ctx->modules) {
+        if (m) (void)hipModuleUnload(m);
+        m = nullptr;
+    }
+    ctx->loaded = false;
 }
 
 struct GemvPlan {
@@ -165,7 +180,7 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
                 const void* ba, const void* bb, void* y, int n, int k, int mode, int act, bool pair,
                 const char* api) {
-    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
     if (n < 0 || k <= 0 || k % F->block_elems)
@@ -218,7 +233,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
 
 extern "C" {
 
-int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
+int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (!out) return fail(CIMA_E_INVALID, "cima_hip_init: null out pointer");
     *out = nullptr;
     int count = 0;
@@ -238,15 +253,20 @@ int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
         delete ctx;
         return hip_fail(e, "hipDeviceGetAttribute(LDS per block)");
     }
-    std::string path = code_object ? std::string(code_object) : default_code_object();
-    if ((e = hipModuleLoad(&ctx->module, path.c_str())) != hipSuccess) {
-        delete ctx;
-        return fail((int)e, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
+    const std::string dir = code_dir ? std::string(code_dir) : default_code_dir();
+    for (int i = 0; i < 3; i++) {
+        const std::string path = dir + "/" + kModuleFiles[i];
+        if ((e = hipModuleLoad(&ctx->modules[i], path.c_str())) != hipSuccess) {
+            unload(ctx);
+            delete ctx;
+            return fail((int)e, "hipModuleLoad(%s) failed: %s", path.c_str(), hipGetErrorString(e));
+        }
     }
+    ctx->loaded = true;
     // resolve every kernel up front (the reference's KernelSet)
-    auto add = [&](const std::string& name) -> int {
+    auto add = [&](int mod, const std::string& name) -> int {
         hipFunction_t f;
-        hipError_t r = hipModuleGetFunction(&f, ctx->module, name.c_str());
+        hipError_t r = hipModuleGetFunction(&f, ctx->modules[mod], name.c_str());
         if (r != hipSuccess) return fail((int)r, "hipModuleGetFunction(%s): %s", name.c_str(), hipGetErrorString(r));
         ctx->fns[name] = f;
         return 0;
@@ -259,18 +279,25 @@ int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out) {
                 for (const char* sfx : {"", "_epi", "_pair", "_pair_epi"}) {
                     char name[96];
                     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
-                    if (!rc) rc = add(name);
+                    if (!rc) rc = add(0, name);
                 }
-        if (!rc) rc = add(std::string("cima_dequant_") + F->name);
-        if (!rc) rc = add(std::string("cima_gather_") + F->name);
+        for (int bn : kGemmBN)
+            for (const char* xt : {"f32", "f16", "bf16"})
+                for (const char* yt : {"f32", "f16"}) {
+                    char name[96];
+                    snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xt, yt);
+                    if (!rc) rc = add(1, name);
+                }
+        if (!rc) rc = add(2, std::string("cima_dequant_") + F->name);
+        if (!rc) rc = add(2, std::string("cima_gather_") + F->name);
     }
     if (rc) {
-        (void)hipModuleUnload(ctx->module);
+        unload(ctx);
         delete ctx;
         return rc;
     }
     if ((e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking)) != hipSuccess) {
-        (void)hipModuleUnload(ctx->module);
+        unload(ctx);
         delete ctx;
         return hip_fail(e, "hipStreamCreateWithFlags");
     }
@@ -296,8 +323,7 @@ int cima_hip_destroy(cima_hip_ctx* ctx) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
     }
-    if (ctx->module) (void)hipModuleUnload(ctx->module);
-    ctx->module = nullptr;
+    unload(ctx);
     delete ctx;
     return 0;
 }
@@ -349,6 +375,15 @@ int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu) {
     return 0;
 }
 
+int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemm_tile: null context");
+    bool ok = tokens == 0;
+    for (int b : kGemmBN) ok = ok || tokens == b;
+    if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 64 or 128", tokens);
+    ctx->tune_gemm_bn = tokens;
+    return 0;
+}
+
 int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lpr) {
     if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_tuning: null context");
     if (rows != 0 && rows != 1 && rows != 2)
@@ -383,8 +418,48 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int t, const void* x, const voi
     return gemv_common(ctx, t, x, wg, wu, bg, bu, y, n, k, 2, act, true, "cima_hip_gguf_gemv_swiglu");
 }
 
+int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
+                       int ldy, int x_dtype, int y_dtype) {
+    const char* api = "cima_hip_gguf_gemm";
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    const Fmt* F = fmt_of(t);
+    if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
+    if (m < 0 || n < 0 || k <= 0 || k % 64 || k % F->block_elems)
+        return fail(CIMA_E_INVALID, "%s: shape m=%d n=%d k=%d: k must be a positive multiple of %d", api, m, n, k,
+                    F->block_elems > 64 ? F->block_elems : 64);
+    if (ldy < n) return fail(CIMA_E_INVALID, "%s: ldy=%d < n=%d", api, ldy, n);
+    if (x_dtype < CIMA_DT_F32 || x_dtype > CIMA_DT_BF16 || (y_dtype != CIMA_DT_F32 && y_dtype != CIMA_DT_F16))
+        return fail(CIMA_E_INVALID, "%s: x_dtype %d / y_dtype %d not supported", api, x_dtype, y_dtype);
+    if (m == 0 || n == 0) return 0;
+    if (!x || !w || !y) return fail(CIMA_E_INVALID, "%s: null x, w or y", api);
+    if (!aligned(x, 8) || !aligned(w, F->w_align) || !aligned(y, 4))
+        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x 8 B, %s weights %d B, y 4 B)", api, F->name,
+                    F->w_align);
+    // token tile: the smallest built width covering m, else 128
+    int bn = 128;
+    for (int b : kGemmBN)
+        if (m <= b) {
+            bn = b;
+            break;
+        }
+    if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
+    static const char* const xn[] = {"f32", "f16", "bf16"};
+    char name[96];
+    snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xn[x_dtype], y_dtype == CIMA_DT_F32 ? "f32" : "f16");
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, name, &f)) return rc;
+    const void* xa = x;
+    const void* wa = w;
+    void* ya = y;
+    int mm = m, nn = n, kk = k, ld = ldy;
+    void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
+    hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + 127) / 128), (unsigned)((m + bn - 1) / bn), 1, 256, 1, 1,
+                                         0, ctx->stream, args, nullptr);
+    return e == hipSuccess ? 0 : hip_fail(e, api);
+}
+
 int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int t, const void* src, void* out, long long nblocks) {
-    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_dequant: context is not initialised");
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_dequant: context is not initialised");
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_dequant: ggml type %d is not a supported GGUF block format", t);
     if (nblocks < 0) return fail(CIMA_E_INVALID, "cima_hip_gguf_dequant: nblocks %lld < 0", nblocks);
@@ -406,7 +481,7 @@ int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int t, const void* src, void* out, 
 
 int cima_hip_gguf_gather(cima_hip_ctx* ctx, int t, const void* table, const unsigned int* ids, void* out, int n,
                          int hidden) {
-    if (!ctx || !ctx->module) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_gather: context is not initialised");
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_gather: context is not initialised");
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_gather: ggml type %d is not a supported GGUF block format", t);
     if (n < 0 || hidden <= 0 || hidden % F->block_elems)

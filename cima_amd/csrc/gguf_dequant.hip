@@ -1,0 +1,47 @@
+// Dequantisation to f16 and packed embedding gather (gfx950 code object
+// cima_dequant.hsaco): one thread per unit of a block, bit-exact with the
+// host decoders (src/quant.rs:599-896).
+#include "gguf_formats.h"
+
+// --------------------------------------------------------- dequant / gather
+// One thread per unit.  dequant: units of a flat run of nblocks blocks,
+// f16 out in element order.  gather: out[i, :] = dequant(table[ids[i]]).
+
+template <typename F>
+__device__ void dequant_body(const uint8_t* __restrict__ src, uint16_t* __restrict__ out, long long nblocks) {
+    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long units = nblocks * F::UPB;
+    if (t >= units) return;
+    long long blk = t / F::UPB;
+    int u = (int)(t % F::UPB);
+    typename F::Raw r = F::load(src + blk * F::BB, u);
+    F::dequant(r, u, out + blk * F::BE + F::out_elem(u));
+}
+
+template <typename F>
+__device__ void gather_body(const uint8_t* __restrict__ table, const uint32_t* __restrict__ ids,
+                            uint16_t* __restrict__ out, int n, int hidden) {
+    long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int upr = hidden / F::UE;  // units per row
+    if (t >= (long long)n * upr) return;
+    int i = (int)(t / upr), u = (int)(t % upr);
+    const size_t row_bytes = (size_t)(hidden / F::BE) * F::BB;
+    typename F::Raw r = F::load(table + (size_t)ids[i] * row_bytes, u);
+    F::dequant(r, u, out + (size_t)i * hidden + F::out_elem(u));
+}
+
+#define DQ_KERNELS(FN, F)                                                                         \
+    extern "C" __global__ __launch_bounds__(256) void cima_dequant_##FN(                          \
+        const uint8_t* src, uint16_t* out, long long nblocks) {                                   \
+        dequant_body<F>(src, out, nblocks);                                                       \
+    }                                                                                             \
+    extern "C" __global__ __launch_bounds__(256) void cima_gather_##FN(                           \
+        const uint8_t* table, const uint32_t* ids, uint16_t* out, int n, int hidden) {            \
+        gather_body<F>(table, ids, out, n, hidden);                                               \
+    }
+
+DQ_KERNELS(q8_0, FQ8_0)
+DQ_KERNELS(q4_0, FQ4_0)
+DQ_KERNELS(q4_k, FQ4_K)
+DQ_KERNELS(q6_k, FQ6_K)
+

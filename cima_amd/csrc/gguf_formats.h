@@ -1,0 +1,262 @@
+// Shared device code of the GGUF kernels for gfx950 (CDNA4): f16 helpers,
+// unaligned loads and the per-format block decoders.  Included by
+// gguf_gemv.hip, gguf_gemm.hip and gguf_dequant.hip, each compiled to its
+// own code object.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DEV __device__ __forceinline__
+
+enum { GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q6_K = 14 };
+enum { ACT_F32 = 0, ACT_F16 = 1 };
+
+// ---------------------------------------------------------------- helpers
+
+DEV float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+// fp32 -> f16 bits with v_cvt_f16_f32 (round to nearest even, f16
+// subnormals kept).  The empty asm makes `v` opaque: without it LLVM folds
+// f16(a * b) into v_fma_mix(a, b, +0), which returns +0 where a * b is -0
+// and, for a * b - c, skips the fp32 rounding the host decoders perform.
+DEV uint32_t f2h(float v) {
+    __asm__("" : "+v"(v));
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+DEV uint4 ld16a(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// 2-byte-aligned 16-byte load: gfx950 runs with unaligned global access
+// enabled, so this is one global_load_dwordx4 (measured at full streaming
+// bandwidth on MI355X), not a byte loop.
+DEV uint4 ld16u(const uint8_t* p) {
+    uint4 v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 16);
+    return v;
+}
+DEV uint32_t ld2(const uint8_t* p) {
+    uint16_t v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 2);
+    return v;
+}
+
+DEV void store32h(uint16_t* out, const uint32_t (&o)[16]) {
+    uint4* p = reinterpret_cast<uint4*>(out);
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+}
+
+// Decoders of one unit to f16 (dequant and gather).  Each value is computed
+// exactly as the host decoder does -- (d*sc)*q [- dmin*m] in fp32, then one
+// RTNE conversion to f16 -- so the bits match.
+
+// --------------------------------------------------------- format: Q8_0
+// block: f16 d, i8 qs[32]; x[i] = d * qs[i]   (src/quant.rs:599-617)
+struct FQ8_0 {
+    static constexpr int BE = 32, BB = 34, UE = 32, UPB = 1;
+    struct Raw { uint4 a, b; uint32_t d; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 34;
+        Raw r;
+        r.d = ld2(blk);
+        r.a = ld16u(blk + 2);
+        r.b = ld16u(blk + 18);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int, uint16_t* out) {
+        float d = h2f(r.d);
+        uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float v0 = d * (float)(int8_t)(w[i] & 0xff), v1 = d * (float)(int8_t)((w[i] >> 8) & 0xff);
+            float v2 = d * (float)(int8_t)((w[i] >> 16) & 0xff), v3 = d * (float)(int8_t)(w[i] >> 24);
+            o[2 * i] = f2h(v0) | (f2h(v1) << 16);
+            o[2 * i + 1] = f2h(v2) | (f2h(v3) << 16);
+        }
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
+};
+
+// --------------------------------------------------------- format: Q4_0
+// block: f16 d, u8 qs[16]; byte j = elem j (low nibble), elem j+16 (high);
+// x = d * (q - 8)   (src/quant.rs:624-644)
+struct FQ4_0 {
+    static constexpr int BE = 32, BB = 18, UE = 32, UPB = 1;
+    struct Raw { uint4 q; uint32_t d; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 18;
+        Raw r;
+        r.d = ld2(blk);
+        r.q = ld16u(blk + 2);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int, uint16_t* out) {
+        float d = h2f(r.d);
+        uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                int b0 = (q[i] >> (16 * j)) & 0xff, b1 = (q[i] >> (16 * j + 8)) & 0xff;
+                float l0 = d * (float)((b0 & 15) - 8), l1 = d * (float)((b1 & 15) - 8);
+                float h0 = d * (float)((b0 >> 4) - 8), h1 = d * (float)((b1 >> 4) - 8);
+                o[2 * i + j] = f2h(l0) | (f2h(l1) << 16);
+                o[8 + 2 * i + j] = f2h(h0) | (f2h(h1) << 16);
+            }
+        }
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
+};
+
+// (sc, m) of sub-blocks 2c and 2c+1 of a Q4_K super-block from its header
+// (dwords y, z, w hold the 12 packed scale bytes), without branches:
+//   j < 4 : sc = s[j] & 63,                        m = s[j+4] & 63
+//   j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4, m = (s[j+4] >> 4) | (s[j] >> 6) << 4
+// (src/quant.rs:731-740)
+DEV void q4k_scales(const uint4& h, int c, uint32_t& sc0, uint32_t& m0, uint32_t& sc1, uint32_t& m1) {
+    const int t = (c & 1) * 16;
+    const uint32_t A = h.y >> t, B = h.z >> t, C = h.w >> t;
+    const bool lo = c < 2;
+    const uint32_t L = lo ? A : C, M = lo ? B : (C >> 4);
+    const uint32_t s6 = lo ? 4 : 6;
+    sc0 = (L & 0xF) | (((A >> s6) & 3) << 4);
+    sc1 = ((L >> 8) & 0xF) | (((A >> (s6 + 8)) & 3) << 4);
+    m0 = (M & 0xF) | (((B >> s6) & 3) << 4);
+    m1 = ((M >> 8) & 0xF) | (((B >> (s6 + 8)) & 3) << 4);
+}
+
+// The same eight (sc, m) pairs decoded all at once, one per byte, then the
+// pair of chunk c picked with one byte permute each (sel = q4k_sel(c)):
+// bytes 0,1 of *sc are sc[2c], sc[2c+1]; of *m, m[2c], m[2c+1].
+DEV uint32_t q4k_sel(int c) { return (uint32_t)(2 * c) | ((uint32_t)(2 * c + 1) << 8) | 0x0c0c0000u; }
+DEV void q4k_scale_pair(const uint4& h, uint32_t sel, uint32_t& sc, uint32_t& m) {
+    const uint32_t sclo = h.y & 0x3F3F3F3Fu;
+    const uint32_t mlo = h.z & 0x3F3F3F3Fu;
+    const uint32_t schi = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    const uint32_t mhi = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+    sc = __builtin_amdgcn_perm(schi, sclo, sel);
+    m = __builtin_amdgcn_perm(mhi, mlo, sel);
+}
+
+// --------------------------------------------------------- format: Q4_K
+// super-block (144 B): f16 d, f16 dmin, u8 scales[12], u8 qs[128].
+// 64-element chunk c uses qs[32c..32c+32): low nibbles are sub-block 2c,
+// high nibbles sub-block 2c+1; x = (d*sc)*q - dmin*m  (src/quant.rs:743-774).
+// Unit u: super-block u/8, qs bytes [16*(u%8), +16) -> chunk c = (u%8)/2,
+// elements c*64 + 16*(u%2) + [0,16) (low) and the same +32 (high).
+struct FQ4_K {
+    static constexpr int BE = 256, BB = 144, UE = 32, UPB = 8;
+    struct Raw { uint4 q; uint4 h; };
+    DEV static int elem0(int u) { return (u >> 3) * 256 + ((u & 7) >> 1) * 64 + (u & 1) * 16; }
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 144;
+        Raw r;
+        r.h = ld16a(blk);
+        r.q = ld16a(blk + 16 + (u & 7) * 16);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int u, uint16_t* out) {
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(r.h, (u & 7) >> 1, sc0, m0, sc1, m1);
+        float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
+        float d0 = d * (float)sc0, mm0 = dmin * (float)m0, d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        uint32_t ol[8], oh[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                uint32_t b0 = (q[i] >> (16 * j)) & 0xff, b1 = (q[i] >> (16 * j + 8)) & 0xff;
+                // (d*sc)*q is exact in fp32, so the subtraction is the only
+                // fp32 rounding -- identical to the host decoder
+                float l0 = d0 * (float)(b0 & 15) - mm0, l1 = d0 * (float)(b1 & 15) - mm0;
+                float h0 = d1 * (float)(b0 >> 4) - mm1, h1 = d1 * (float)(b1 >> 4) - mm1;
+                ol[2 * i + j] = f2h(l0) | (f2h(l1) << 16);
+                oh[2 * i + j] = f2h(h0) | (f2h(h1) << 16);
+            }
+        }
+        uint4* pl = reinterpret_cast<uint4*>(out);
+        uint4* ph = reinterpret_cast<uint4*>(out + 32);
+        pl[0] = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+        pl[1] = make_uint4(ol[4], ol[5], ol[6], ol[7]);
+        ph[0] = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+        ph[1] = make_uint4(oh[4], oh[5], oh[6], oh[7]);
+    }
+    DEV static int out_elem(int u) { return elem0(u); }
+};
+
+// --------------------------------------------------------- format: Q6_K
+// super-block (210 B): u8 ql[128], u8 qh[64], i8 sc[16], f16 d (at 208).
+// Half h (128 elements), l in [0,32): elements +l, +l+32, +l+64, +l+96 take
+// (low ql[64h+l], low ql[64h+l+32], high ql[64h+l], high ql[64h+l+32]) with
+// qh[32h+l] bits (0-1, 2-3, 4-5, 6-7) as bits 4-5, minus 32; scale
+// sc[8h + l/16 + 2g]; x = (d*sc)*q   (src/quant.rs:857-896).
+// Unit u: super-block u/4, half h = (u/2)%2, l in 16*(u%2) + [0,16): four
+// groups g of 16 consecutive elements.
+struct FQ6_K {
+    static constexpr int BE = 256, BB = 210, UE = 64, UPB = 4;
+    struct Raw { uint4 a, b, h; uint2 sc; uint32_t d; };
+    DEV static int elem0(int u) { return (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16; }
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 2) * 210;
+        const int hh = (u >> 1) & 1, is = u & 1;
+        Raw r;
+        r.a = ld16u(blk + hh * 64 + is * 16);
+        r.b = ld16u(blk + hh * 64 + 32 + is * 16);
+        r.h = ld16u(blk + 128 + hh * 32 + is * 16);
+        __builtin_memcpy(&r.sc, __builtin_assume_aligned(blk + 192 + hh * 8, 2), 8);
+        r.d = ld2(blk + 208);
+        return r;
+    }
+    // 6-bit quants (0..63) of group g, one per byte in element order
+    DEV static void q6(const Raw& r, uint32_t (&q)[4][4]) {
+        uint32_t a[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+        uint32_t b[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+        uint32_t h[4] = {r.h.x, r.h.y, r.h.z, r.h.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            q[0][i] = (a[i] & 0x0F0F0F0Fu) | ((h[i] << 4) & 0x30303030u);
+            q[1][i] = (b[i] & 0x0F0F0F0Fu) | ((h[i] << 2) & 0x30303030u);
+            q[2][i] = ((a[i] >> 4) & 0x0F0F0F0Fu) | (h[i] & 0x30303030u);
+            q[3][i] = ((b[i] >> 4) & 0x0F0F0F0Fu) | ((h[i] >> 2) & 0x30303030u);
+        }
+    }
+    // int8 scales of the unit's four groups: sc[8hh + is + 2g]
+    DEV static void scales(const Raw& r, int u, float (&s)[4]) {
+        const int sh = 8 * (u & 1);
+        s[0] = (float)(int8_t)(r.sc.x >> sh);
+        s[1] = (float)(int8_t)(r.sc.x >> (sh + 16));
+        s[2] = (float)(int8_t)(r.sc.y >> sh);
+        s[3] = (float)(int8_t)(r.sc.y >> (sh + 16));
+    }
+    DEV static void dequant(const Raw& r, int u, uint16_t* out) {
+        uint32_t q[4][4];
+        q6(r, q);
+        float s[4];
+        scales(r, u, s);
+        float d = h2f(r.d);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            float ds = d * s[g];  // exact: 11-bit x 8-bit
+            uint32_t o[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float v0 = ds * (float)((int)((q[g][i]) & 0xff) - 32);
+                float v1 = ds * (float)((int)((q[g][i] >> 8) & 0xff) - 32);
+                float v2 = ds * (float)((int)((q[g][i] >> 16) & 0xff) - 32);
+                float v3 = ds * (float)((int)((q[g][i] >> 24) & 0xff) - 32);
+                o[2 * i] = f2h(v0) | (f2h(v1) << 16);
+                o[2 * i + 1] = f2h(v2) | (f2h(v3) << 16);
+            }
+            uint4* p = reinterpret_cast<uint4*>(out + 32 * g);
+            p[0] = make_uint4(o[0], o[1], o[2], o[3]);
+            p[1] = make_uint4(o[4], o[5], o[6], o[7]);
+        }
+    }
+    DEV static int out_elem(int u) { return elem0(u); }
+};
+

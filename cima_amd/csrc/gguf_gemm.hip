@@ -1,0 +1,251 @@
+#include "gguf_formats.h"
+
+// ------------------------------------------------------- prefill GEMM (MFMA)
+//
+// Y[m, n] (row stride ldy) = X[m, k] . W[n, k]^T: X holds m tokens, W is the
+// packed GGUF weight (the engine's lin_gemm, src/models/transformer.rs:
+// 618-655, which dequantises W to an f16 slab and runs an f16 GEMM).
+// Each stage of 64 k, a 256-thread workgroup dequantises its 128 weight
+// rows x 64 k to f16 in LDS -- bit-exact with the host decoders, so the
+// operand equals the reference's dequantised weight -- stages the X tile as
+// f16 (bf16 -> f16 is exact for |x| >= 2^-14), and runs
+// v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Wave w owns weight rows
+// [32w, 32w+32) of the tile and all BN tokens.  LDS is double-buffered: the
+// global loads of stage s+1 are in flight while stage s is multiplied.
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+enum { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2 };
+
+// 32 contiguous elements [32j, 32j+32) of a row -> f16 bits, 2 per dword,
+// computed exactly as the host decoders do
+struct DQ8_0 {
+    static constexpr int BE = 32, BB = 34;
+    using Raw = FQ8_0::Raw;
+    DEV static Raw load(const uint8_t* row, int j) { return FQ8_0::load(row, j); }
+    DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        const float d = h2f(r.d);
+        const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o[2 * i] = f2h(d * (float)(int8_t)(w[i] & 0xff)) | (f2h(d * (float)(int8_t)((w[i] >> 8) & 0xff)) << 16);
+            o[2 * i + 1] = f2h(d * (float)(int8_t)((w[i] >> 16) & 0xff)) | (f2h(d * (float)(int8_t)(w[i] >> 24)) << 16);
+        }
+    }
+};
+struct DQ4_0 {
+    static constexpr int BE = 32, BB = 18;
+    using Raw = FQ4_0::Raw;
+    DEV static Raw load(const uint8_t* row, int j) { return FQ4_0::load(row, j); }
+    DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        const float d = h2f(r.d);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int jj = 0; jj < 2; jj++) {
+                const int b0 = (q[i] >> (16 * jj)) & 0xff, b1 = (q[i] >> (16 * jj + 8)) & 0xff;
+                o[2 * i + jj] = f2h(d * (float)((b0 & 15) - 8)) | (f2h(d * (float)((b1 & 15) - 8)) << 16);
+                o[8 + 2 * i + jj] = f2h(d * (float)((b0 >> 4) - 8)) | (f2h(d * (float)((b1 >> 4) - 8)) << 16);
+            }
+        }
+    }
+};
+// sub-block j: super-block j/8, sub s = j%8 -> qs bytes 32*(s/2) + [0,32),
+// low nibbles if s is even, high if odd
+struct DQ4_K {
+    static constexpr int BE = 256, BB = 144;
+    struct Raw { uint4 h, q0, q1; };
+    DEV static Raw load(const uint8_t* row, int j) {
+        const uint8_t* blk = row + (size_t)(j >> 3) * 144;
+        const int c = (j & 7) >> 1;
+        Raw r;
+        r.h = ld16a(blk);
+        r.q0 = ld16a(blk + 16 + 32 * c);
+        r.q1 = ld16a(blk + 32 + 32 * c);
+        return r;
+    }
+    DEV static void deq(const Raw& r, int j, uint32_t (&o)[16]) {
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(r.h, (j & 7) >> 1, sc0, m0, sc1, m1);
+        const bool hi = j & 1;
+        const float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
+        const float ds = d * (float)(hi ? sc1 : sc0), mm = dmin * (float)(hi ? m1 : m0);
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t n = hi ? ((q[i] >> 4) & 0x0F0F0F0Fu) : (q[i] & 0x0F0F0F0Fu);
+            // (d*sc)*q is exact, so the subtraction is the only fp32 rounding
+            o[2 * i] = f2h(ds * (float)(n & 0xff) - mm) | (f2h(ds * (float)((n >> 8) & 0xff) - mm) << 16);
+            o[2 * i + 1] = f2h(ds * (float)((n >> 16) & 0xff) - mm) | (f2h(ds * (float)(n >> 24) - mm) << 16);
+        }
+    }
+};
+// sub-block j: super-block j/8, r = j%8 -> half h = r/4, group g = r%4:
+// l in [0,32) takes nibble (g<2 low, else high) of ql[64h + 32(g&1) + l],
+// bits 2g..2g+1 of qh[32h + l], scale sc[8h + l/16 + 2g]
+struct DQ6_K {
+    static constexpr int BE = 256, BB = 210;
+    struct Raw { uint4 a0, a1, h0, h1; uint32_t sc, d; };
+    DEV static Raw load(const uint8_t* row, int j) {
+        const uint8_t* blk = row + (size_t)(j >> 3) * 210;
+        const int hh = (j & 7) >> 2, g = j & 3;
+        Raw r;
+        r.a0 = ld16u(blk + 64 * hh + 32 * (g & 1));
+        r.a1 = ld16u(blk + 64 * hh + 32 * (g & 1) + 16);
+        r.h0 = ld16u(blk + 128 + 32 * hh);
+        r.h1 = ld16u(blk + 128 + 32 * hh + 16);
+        r.sc = ld2(blk + 192 + 8 * hh + 2 * g);  // sc[8h + 2g], sc[8h + 2g + 1]
+        r.d = ld2(blk + 208);
+        return r;
+    }
+    DEV static void deq(const Raw& r, int j, uint32_t (&o)[16]) {
+        const int g = j & 3;
+        const int nsh = g < 2 ? 0 : 4, hsh = 2 * g;
+        const float d = h2f(r.d);
+        const float ds0 = d * (float)(int8_t)(r.sc & 0xff), ds1 = d * (float)(int8_t)(r.sc >> 8);
+        const uint32_t a[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
+        const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float ds = i < 4 ? ds0 : ds1;
+            const uint32_t q = ((a[i] >> nsh) & 0x0F0F0F0Fu) | (((h[i] >> hsh) & 0x03030303u) << 4);
+            o[2 * i] = f2h(ds * (float)((int)(q & 0xff) - 32)) | (f2h(ds * (float)((int)((q >> 8) & 0xff) - 32)) << 16);
+            o[2 * i + 1] = f2h(ds * (float)((int)((q >> 16) & 0xff) - 32)) | (f2h(ds * (float)((int)(q >> 24) - 32)) << 16);
+        }
+    }
+};
+
+constexpr int GBM = 128;        // weight rows per workgroup
+constexpr int GBK = 64;         // k per stage
+constexpr int GKP = GBK + 8;    // LDS row pitch in halves (pads away bank conflicts)
+
+template <int XT>
+DEV uint32_t x_pair_f16(const void* x, size_t i) {  // elements i, i+1 -> packed f16
+    if constexpr (XT == XT_F16) {
+        return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
+    } else if constexpr (XT == XT_BF16) {
+        const uint32_t b = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
+        return f2h(__builtin_bit_cast(float, b << 16)) | (f2h(__builtin_bit_cast(float, b & 0xffff0000u)) << 16);
+    } else {
+        const float2 v = *reinterpret_cast<const float2*>(static_cast<const float*>(x) + i);
+        return f2h(v.x) | (f2h(v.y) << 16);
+    }
+}
+
+template <typename D, int BN, int XT, int YT>
+__device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
+                          int m, int n, int k, int ldy) {
+    __shared__ __align__(16) uint16_t wl[2][GBM * GKP];
+    __shared__ __align__(16) uint16_t xl[2][BN * GKP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * GBM, t0 = blockIdx.y * BN;
+    const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const int nk = k / GBK;
+
+    // weight: thread t dequantises sub-block 2*kb + (t & 1) of tile row t >> 1
+    const int wrow = tid >> 1, wsub = tid & 1;
+    const int grow = min(r0 + wrow, n - 1);
+    const uint8_t* wp = w + (size_t)grow * row_bytes;
+    // activations: BN x 64 halves per stage = BN * 32 pairs
+    constexpr int XPAIRS = BN * GBK / 2;
+    constexpr int XPT = (XPAIRS + 255) / 256;  // pairs per thread
+    typename D::Raw wr = D::load(wp, 2 * 0 + wsub);
+    uint32_t xr[XPT];
+    auto load_x = [&](int kb) {
+#pragma unroll
+        for (int p = 0; p < XPT; p++) {
+            const int pi = tid + 256 * p;
+            const int tok = pi / (GBK / 2), kk = 2 * (pi % (GBK / 2));
+            const int gt = min(t0 + tok, m - 1);
+            xr[p] = (pi < XPAIRS) ? x_pair_f16<XT>(x, (size_t)gt * k + (size_t)kb * GBK + kk) : 0u;
+        }
+    };
+    load_x(0);
+
+    float4_t acc[2][BN / 16];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < BN / 16; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < nk; kb++) {
+        const int buf = kb & 1;
+        {   // dequantised weights -> LDS
+            uint32_t o[16];
+            D::deq(wr, 2 * kb + wsub, o);
+            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * GKP + 32 * wsub]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        }
+#pragma unroll
+        for (int p = 0; p < XPT; p++) {  // activations -> LDS (tokens past m are copies, never stored)
+            const int pi = tid + 256 * p;
+            if (pi < XPAIRS) {
+                const int tok = pi / (GBK / 2), kk = 2 * (pi % (GBK / 2));
+                *reinterpret_cast<uint32_t*>(&xl[buf][tok * GKP + kk]) = xr[p];
+            }
+        }
+        __syncthreads();
+        if (kb + 1 < nk) {
+            wr = D::load(wp, 2 * (kb + 1) + wsub);
+            load_x(kb + 1);
+        }
+#pragma unroll
+        for (int ks = 0; ks < GBK / 32; ks++) {
+            const int kof = 32 * ks + 8 * (lane >> 4);
+            half8_t av[2];
+#pragma unroll
+            for (int a = 0; a < 2; a++)
+                av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(32 * wave + 16 * a + (lane & 15)) * GKP + kof]);
+#pragma unroll
+            for (int b = 0; b < BN / 16; b++) {
+                const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * GKP + kof]);
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
+            }
+        }
+    }
+
+    // lane holds D[4*(lane/16) + i][lane%16] of each 16x16 tile:
+    // weight row r0 + 32*wave + 16*a + 4*(lane/16) + i, token t0 + 16*b + lane%16
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+#pragma unroll
+        for (int b = 0; b < BN / 16; b++) {
+            const int tok = t0 + 16 * b + (lane & 15);
+            const int rb = r0 + 32 * wave + 16 * a + 4 * (lane >> 4);
+            if (tok < m) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (rb + i < n) {
+                        const size_t off = (size_t)tok * ldy + rb + i;
+                        if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = acc[a][b][i];
+                        else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(acc[a][b][i]);
+                    }
+                }
+            }
+        }
+    }
+}
+
+// name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
+#define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
+    extern "C" __global__ __launch_bounds__(256) void cima_gemm_##FN##_b##BN##_##XN##_##YN(          \
+        const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
+        gemm_body<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                           \
+    }
+#define GEMM_XY(FN, D, BN)                                                    \
+    GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F32, f32)                          \
+    GEMM_KERNEL(FN, D, BN, XT_F16, f16, XT_F32, f32)                          \
+    GEMM_KERNEL(FN, D, BN, XT_BF16, bf16, XT_F32, f32)                        \
+    GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F16, f16)                          \
+    GEMM_KERNEL(FN, D, BN, XT_F16, f16, XT_F16, f16)                          \
+    GEMM_KERNEL(FN, D, BN, XT_BF16, bf16, XT_F16, f16)
+#define GEMM_FMT(FN, D) GEMM_XY(FN, D, 16) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
+
+GEMM_FMT(q8_0, DQ8_0)
+GEMM_FMT(q4_0, DQ4_0)
+GEMM_FMT(q4_k, DQ4_K)
+GEMM_FMT(q6_k, DQ6_K)

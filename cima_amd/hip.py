@@ -24,15 +24,15 @@ from . import gguf
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 LIBHIP = os.path.join(LIB_DIR, "libcima_hip.so")
-HSACO = os.path.join(LIB_DIR, "cima_gguf.hsaco")
+CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco") for n in ("gemv", "gemm", "dequant")]
 
 # declared in include/cima_hip.h, in order
 EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
-    "cima_hip_set_gemv_grid",
+    "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv",
-    "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
+    "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
 )
 
 E_INVALID, E_FORMAT, E_NO_KERNEL, E_NOT_INIT = -1, -2, -3, -4
@@ -71,8 +71,10 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_num_cu.argtypes = [P]
     L.cima_hip_set_gemv_tuning.argtypes = [P, I, I]
     L.cima_hip_set_gemv_grid.argtypes = [P, I]
+    L.cima_hip_set_gemm_tile.argtypes = [P, I]
     L.cima_hip_gguf_gemv.argtypes = [P, I, P, P, P, P, I, I, I, I]
     L.cima_hip_gguf_gemv_swiglu.argtypes = [P, I, P, P, P, P, P, P, I, I, I]
+    L.cima_hip_gguf_gemm.argtypes = [P, I, P, P, P, I, I, I, I, I, I]
     L.cima_hip_gguf_dequant.argtypes = [P, I, P, P, LL]
     L.cima_hip_gguf_gather.argtypes = [P, I, P, P, P, I, I]
     _lib = L
@@ -106,12 +108,14 @@ def _act_of(t) -> int:
 class HipCtx:
     """One device context: a loaded gfx950 module and a launch stream."""
 
-    def __init__(self, device: int = 0, code_object: Optional[str] = None):
+    def __init__(self, device: int = 0, code_dir: Optional[str] = None):
         self.lib = load_library()
-        if code_object is None and not os.path.exists(HSACO):
-            raise EngineError("hip", E_NOT_INIT, f"{HSACO} is not built (run python -m cima_amd.build)")
+        if code_dir is None:
+            missing = [p for p in CODE_OBJECTS if not os.path.exists(p)]
+            if missing:
+                raise EngineError("hip", E_NOT_INIT, f"{missing[0]} is not built (run python -m cima_amd.build)")
         h = ctypes.c_void_p()
-        co = (code_object or HSACO).encode()
+        co = (code_dir or LIB_DIR).encode()
         self._check(self.lib.cima_hip_init(device, co, ctypes.byref(h)))
         self.handle = h
         self.device = device
@@ -179,6 +183,21 @@ class HipCtx:
             act_dtype = _act_of(x) if hasattr(x, "dtype") else gguf.DT_F32
         self._check(self.lib.cima_hip_gguf_gemv_swiglu(self.handle, int(fmt), _ptr(x), _ptr(w_gate), _ptr(w_up),
                                                        _ptr(bias_gate), _ptr(bias_up), _ptr(y), n, k, act_dtype))
+
+    def gguf_gemm(self, fmt: int, x, w, y, m: int, n: int, k: int, ldy: Optional[int] = None,
+                  x_dtype: Optional[int] = None, y_dtype: Optional[int] = None) -> None:
+        """``Y[m,n] = X[m,k]·dequant(W)[n,k]^T`` (prefill, MFMA); ldy defaults to n."""
+        def dt(t, default):
+            if t is not None:
+                return t
+            import torch
+
+            return {torch.float32: gguf.DT_F32, torch.float16: gguf.DT_F16,
+                    torch.bfloat16: gguf.DT_BF16}.get(getattr(x if default == "x" else y, "dtype", None), gguf.DT_F32)
+        xd = dt(x_dtype, "x") if hasattr(x, "dtype") or x_dtype is not None else gguf.DT_F32
+        yd = dt(y_dtype, "y") if hasattr(y, "dtype") or y_dtype is not None else gguf.DT_F32
+        self._check(self.lib.cima_hip_gguf_gemm(self.handle, int(fmt), _ptr(x), _ptr(w), _ptr(y), m, n, k,
+                                                n if ldy is None else ldy, xd, yd))
 
     def gguf_dequant(self, fmt: int, src, out, nblocks: int) -> None:
         """Decode ``nblocks`` blocks to f16 (bit-exact with the host decoders)."""

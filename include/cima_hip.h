@@ -47,11 +47,12 @@ typedef struct cima_hip_ctx cima_hip_ctx;
 
 /* Context creation: replaces CudaCtx::init (src/cuda.rs:691-908) -- device
  * selection, one non-blocking stream, then loading the prebuilt gfx950 code
- * object with hipModuleLoad and resolving every kernel (the reference
- * JIT-compiles with NVRTC and resolves its KernelSet, src/cuda.rs:808-877).
- * code_object: path of cima_gguf.hsaco, or NULL for the file next to this
- * library. */
-int cima_hip_init(int device, const char* code_object, cima_hip_ctx** out);
+ * objects (cima_gemv.hsaco, cima_gemm.hsaco, cima_dequant.hsaco) with
+ * hipModuleLoad and resolving every kernel (the reference JIT-compiles with
+ * NVRTC and resolves its KernelSet, src/cuda.rs:808-877).
+ * code_dir: directory holding the code objects, or NULL for the directory
+ * of this library. */
+int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out);
 
 /* Releases the module and the context's own stream. */
 int cima_hip_destroy(cima_hip_ctx* ctx);
@@ -90,6 +91,11 @@ int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
  * if fewer fit; environment variable CIMA_GEMV_WGS at init). */
 int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
+/* Prefill GEMM tuning (no counterpart in the reference): token-tile width
+ * (16, 64 or 128) for later gguf_gemm calls; 0 = the smallest built width
+ * covering m (128 beyond). */
+int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
+
 /* Fused dequant-GEMV: replaces CudaCtx::gguf_gemv (src/cuda.rs:2161-2220).
  *   y[r] = sum_j W[r, j] * x[j] for r in [0, n), W packed GGUF rows of k
  *   elements (row r at r * storage_bytes(fmt, k)).
@@ -114,6 +120,18 @@ int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const void* x, const vo
 int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
                               const void* w_gate, const void* w_up, const void* bias_gate,
                               const void* bias_up, void* y, int n, int k, int act_dtype);
+
+/* Prefill dequant-GEMM on MFMA: Y[m, n] (row stride ldy >= n) =
+ * X[m, k] . dequant(W)[n, k]^T for m tokens.  Replaces the reference's
+ * lin_gemm (src/models/transformer.rs:618-655): gguf_dequant of W into an
+ * f16 slab (src/cuda.rs:2285) followed by gemm_f16 / gemm_strided_out
+ * (src/cuda.rs:2468-2570), with no slab -- W is dequantised tile by tile
+ * into LDS, bit-exact f16, and multiplied with f16 MFMA, fp32 accumulate.
+ * x_dtype: CIMA_DT_F32, CIMA_DT_F16 or CIMA_DT_BF16 (converted to f16;
+ * exact for |x| >= 2^-14); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
+ * Requires k % 64 == 0 (and k % 256 for K-quants), x 8-byte aligned. */
+int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
+                       int m, int n, int k, int ldy, int x_dtype, int y_dtype);
 
 /* Dequantise nblocks consecutive blocks to f16, bit-exact with the host
  * decoders: replaces CudaCtx::gguf_dequant (src/cuda.rs:2285-2320). */

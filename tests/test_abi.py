@@ -38,16 +38,24 @@ def test_python_binding_covers_header():
 
 
 def test_code_object_holds_every_kernel():
-    blob = open(cbuild.HSACO, "rb").read()
-    assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+    blobs = {}
+    for name, path in cbuild.HSACOS.items():
+        blob = open(path, "rb").read()
+        assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
+        assert b"gfx950" in blob
+        blobs[name] = blob
     for f in ("q8_0", "q4_0", "q4_k", "q6_k"):
+        blob = blobs["gemv"]
         for r, it in ((1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4)):
             for a in ("f32", "f16"):
                 for sfx in ("", "_epi", "_pair", "_pair_epi"):
                     assert f"cima_gemv_{f}_r{r}_i{it}_{a}{sfx}".encode() in blob
-        assert f"cima_dequant_{f}".encode() in blob
-        assert f"cima_gather_{f}".encode() in blob
-    assert b"gfx950" in blob
+        assert f"cima_dequant_{f}".encode() in blobs["dequant"]
+        assert f"cima_gather_{f}".encode() in blobs["dequant"]
+        for bn in (16, 64, 128):
+            for xt in ("f32", "f16", "bf16"):
+                for yt in ("f32", "f16"):
+                    assert f"cima_gemm_{f}_b{bn}_{xt}_{yt}".encode() in blobs["gemm"]
 
 
 def test_error_classification():
