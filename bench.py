@@ -45,6 +45,8 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=4, help="layer steps in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 decode-step leg")
+    ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--calib", action="store_true",
                     help="also run a 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     return ap.parse_args()
@@ -216,6 +218,44 @@ def main():
                 "kernel": "cima_gemv_q4_k_r1_i1_f32_pair", "alg_bytes_per_launch": pair_bytes,
                 "avg_launch_us": round(pair_us, 3)}
 
+    # ---- config 5: whole greedy decode step of a Qwen2.5-0.5B-shaped Q8_0
+    # model, KV prefilled to 2048, one graph replay per token
+    decode = None
+    if not args.no_decode:
+        from cima_amd.decoder import DecoderConfig, DeviceDecoder, synthetic_kv, synthetic_model
+
+        dcfg = DecoderConfig()
+        dm = synthetic_model(dcfg, seed=5)
+        dd = DeviceDecoder(ctx, dm)
+        ctx_len = 2048
+        for i in range(dcfg.n_layers):
+            dd.load_kv(i, *synthetic_kv(dcfg, i, ctx_len))
+        wbytes_tok = dm.embed.nbytes + sum(sum(v.nbytes for v in L.values() if v is not None) for L in dm.layers)
+        del dm
+        dd.set_state(1, ctx_len)
+        dd.capture()
+        for _ in range(20):
+            dd.replay()
+        torch.cuda.synchronize()
+        p0 = dd.position()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(args.decode_tokens):
+            dd.replay()
+        b.record()
+        torch.cuda.synchronize()
+        dms = a.elapsed_time(b) / args.decode_tokens
+        assert dd.position() == p0 + args.decode_tokens
+        kv_bytes = dcfg.n_layers * 2 * dcfg.kv_heads * dcfg.head_dim * 2 * (p0 + args.decode_tokens // 2)
+        decode = {"workload": "qwen2.5-0.5b-shaped Q8_0 greedy decode step (24 layers, tied 151936 head), "
+                              "KV prefilled to 2048, one hipGraph replay per token (5 launches/layer + 4)",
+                  "tok_s": round(1e3 / dms, 1), "ms_per_token": round(dms, 4), "tokens": args.decode_tokens,
+                  "context": [p0, p0 + args.decode_tokens],
+                  "bytes_per_token": wbytes_tok + kv_bytes,
+                  "gb_s": round((wbytes_tok + kv_bytes) / dms / 1e6, 1)}
+        del dd
+        torch.cuda.empty_cache()
+
     # ---- CPU baseline: the reference's host path on a bounded sample
     cpu = None
     if not args.no_cpu:
@@ -256,6 +296,7 @@ def main():
                    "hbm_frac_of_8TBs": round(value / PEAK_HBM_GBS, 4),
                    "wall_s": round(wall, 3)},
         "shapes": shapes_out,
+        "decode_step": decode,
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

@@ -3,7 +3,8 @@
 Produces, in ``cima_amd/lib/``:
   cima_gemv.hsaco     gfx950 code objects (hipcc --genco): decode GEMVs,
   cima_gemm.hsaco       prefill dequant-GEMMs (MFMA),
-  cima_dequant.hsaco    dequant-to-f16 and packed gather
+  cima_dequant.hsaco    dequant-to-f16 and packed gather,
+  cima_decode.hsaco     decode-step support (norm, RoPE, attention, argmax)
   libcima_hip.so      host C ABI (include/cima_hip.h), links libamdhip64
   libcima_synth.so    seeded synthetic weights + quantisers (include/cima_synth.h)
 
@@ -24,7 +25,10 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-HSACOS = {name: os.path.join(LIB, f"cima_{name}.hsaco") for name in ("gemv", "gemm", "dequant")}
+# code object -> HIP source
+SOURCES = {"gemv": "gguf_gemv.hip", "gemm": "gguf_gemm.hip", "dequant": "gguf_dequant.hip",
+           "decode": "decode_ops.hip"}
+HSACOS = {name: os.path.join(LIB, f"cima_{name}.hsaco") for name in SOURCES}
 LIBHIP = os.path.join(LIB, "libcima_hip.so")
 LIBSYNTH = os.path.join(LIB, "libcima_synth.so")
 
@@ -42,7 +46,7 @@ HIPCC_FLAGS = [
 def _cmds():
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     return {
-        **{path: [hipcc, *HIPCC_FLAGS, f"-I{CSRC}", "--genco", "-o", path, os.path.join(CSRC, f"gguf_{name}.hip")]
+        **{path: [hipcc, *HIPCC_FLAGS, f"-I{CSRC}", "--genco", "-o", path, os.path.join(CSRC, SOURCES[name])]
            for name, path in HSACOS.items()},
         LIBHIP: ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
                  f"-I{INCLUDE}", f"-I{ROCM}/include", os.path.join(CSRC, "cima_hip.cpp"),

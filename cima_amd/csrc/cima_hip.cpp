@@ -14,6 +14,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdint.h>
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -86,7 +87,7 @@ struct cima_hip_ctx {
     int device = 0;
     int num_cu = 0;
     int max_lds = 0;  // bytes of LDS one workgroup may use
-    hipModule_t modules[3] = {nullptr, nullptr, nullptr};  // gemv, gemm, dequant
+    hipModule_t modules[4] = {nullptr, nullptr, nullptr, nullptr};  // gemv, gemm, dequant, decode
     bool loaded = false;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
@@ -114,7 +115,14 @@ int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, vo
     return 0;
 }
 
-const char* const kModuleFiles[3] = {"cima_gemv.hsaco", "cima_gemm.hsaco", "cima_dequant.hsaco"};
+const char* const kModuleFiles[4] = {"cima_gemv.hsaco", "cima_gemm.hsaco", "cima_dequant.hsaco",
+                                     "cima_decode.hsaco"};
+
+// decode-step kernels (cima_decode.hsaco)
+const char* const kDecodeKernels[] = {
+    "cima_rmsnorm_f16",     "cima_rope_f16",        "cima_kv_append_f16",    "cima_attn_split_d64",
+    "cima_attn_reduce_d64", "cima_attn_decode_d64", "cima_attn_split_d128",  "cima_attn_reduce_d128",
+    "cima_attn_decode_d128", "cima_argmax_f16",     "cima_argmax_to_ids",    "cima_pos_bump"};
 
 std::string default_code_dir() {
     Dl_info info;
@@ -179,7 +187,7 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
                 const void* ba, const void* bb, void* y, int n, int k, int mode, int act, bool pair,
-                const char* api) {
+                const char* api, const void* norm_w = nullptr, float eps = 0.f) {
     if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
@@ -191,6 +199,8 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (!pair && mode != 0 && mode != 1) return fail(CIMA_E_INVALID, "%s: mode %d is not 0, 1 or 2", api, mode);
     if (n == 0) return 0;
     if (!x || !wa || !y || (pair && !wb)) return fail(CIMA_E_INVALID, "%s: null x, w or y", api);
+    if (norm_w && (!aligned(norm_w, 16) || !(eps >= 0.f)))
+        return fail(CIMA_E_INVALID, "%s: norm weight must be 16-byte aligned and eps >= 0", api);
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(wa, F->w_align) || (pair && !aligned(wb, F->w_align)))
         return fail(CIMA_E_INVALID, "%s: misaligned pointer (x needs 16 B, %s weights %d B)", api, F->name,
                     F->w_align);
@@ -224,8 +234,10 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     const void* b0 = ba;
     const void* b1 = bb;
     void* yy = y;
+    const void* nw = norm_w;
+    float ep = eps;
     int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
-    void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls};
+    void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls, &nw, &ep};
     return launch(ctx, f, p.grid, 256, args, api, p.lds);
 }
 
@@ -254,7 +266,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         return hip_fail(e, "hipDeviceGetAttribute(LDS per block)");
     }
     const std::string dir = code_dir ? std::string(code_dir) : default_code_dir();
-    for (int i = 0; i < 3; i++) {
+    for (int i = 0; i < 4; i++) {
         const std::string path = dir + "/" + kModuleFiles[i];
         if ((e = hipModuleLoad(&ctx->modules[i], path.c_str())) != hipSuccess) {
             unload(ctx);
@@ -291,6 +303,8 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         if (!rc) rc = add(2, std::string("cima_dequant_") + F->name);
         if (!rc) rc = add(2, std::string("cima_gather_") + F->name);
     }
+    for (const char* kn : kDecodeKernels)
+        if (!rc) rc = add(3, kn);
     if (rc) {
         unload(ctx);
         delete ctx;
@@ -395,22 +409,34 @@ int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lpr) {
     return 0;
 }
 
-int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int t, const void* x, const void* w, const void* bias, void* y, int n,
-                       int k, int mode, int act) {
+namespace {
+int gemv_entry(cima_hip_ctx* ctx, int t, const void* x, const void* norm_w, float eps, const void* w,
+               const void* bias, void* y, int n, int k, int mode, int act, const char* api) {
     if (mode == 2) {
         // gate|up pair stored as one [2n, k] weight; bias has 2n entries
         const Fmt* F = fmt_of(t);
-        if (!F) return fail(CIMA_E_FORMAT, "cima_hip_gguf_gemv: ggml type %d is not a supported GGUF block format", t);
+        if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
         if (k <= 0 || k % F->block_elems)
-            return fail(CIMA_E_INVALID, "cima_hip_gguf_gemv: k=%d must be a positive multiple of %d", k,
-                        F->block_elems);
+            return fail(CIMA_E_INVALID, "%s: k=%d must be a positive multiple of %d", api, k, F->block_elems);
         size_t row_bytes = (size_t)(k / F->block_elems) * F->block_bytes;
         size_t esz = act == CIMA_DT_F32 ? 4 : 2;
         const char* wu = w ? (const char*)w + (size_t)(n > 0 ? n : 0) * row_bytes : nullptr;
         const char* bu = bias ? (const char*)bias + (size_t)(n > 0 ? n : 0) * esz : nullptr;
-        return gemv_common(ctx, t, x, w, wu, bias, bu, y, n, k, 2, act, true, "cima_hip_gguf_gemv");
+        return gemv_common(ctx, t, x, w, wu, bias, bu, y, n, k, 2, act, true, api, norm_w, eps);
     }
-    return gemv_common(ctx, t, x, w, nullptr, bias, nullptr, y, n, k, mode, act, false, "cima_hip_gguf_gemv");
+    return gemv_common(ctx, t, x, w, nullptr, bias, nullptr, y, n, k, mode, act, false, api, norm_w, eps);
+}
+}  // namespace
+
+int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int t, const void* x, const void* w, const void* bias, void* y, int n,
+                       int k, int mode, int act) {
+    return gemv_entry(ctx, t, x, nullptr, 0.f, w, bias, y, n, k, mode, act, "cima_hip_gguf_gemv");
+}
+
+int cima_hip_rmsnorm_gguf_gemv(cima_hip_ctx* ctx, int t, const void* x, const void* norm_w, float eps,
+                               const void* w, const void* bias, void* y, int n, int k, int mode, int act) {
+    if (!norm_w) return fail(CIMA_E_INVALID, "cima_hip_rmsnorm_gguf_gemv: null norm weight");
+    return gemv_entry(ctx, t, x, norm_w, eps, w, bias, y, n, k, mode, act, "cima_hip_rmsnorm_gguf_gemv");
 }
 
 int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int t, const void* x, const void* wg, const void* wu,
@@ -502,6 +528,194 @@ int cima_hip_gguf_gather(cima_hip_ctx* ctx, int t, const void* table, const unsi
     int nn = n, hh = hidden;
     void* args[] = {&tb, &id, &o, &nn, &hh};
     return launch(ctx, f, (unsigned)grid, 256, args, "cima_hip_gguf_gather");
+}
+
+
+// ------------------------------------------------------------ decode step
+
+namespace {
+
+const char* const kApiRms = "cima_hip_rmsnorm";
+
+int ready(cima_hip_ctx* ctx, const char* api) {
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    return 0;
+}
+
+int launch_named(cima_hip_ctx* ctx, const char* name, unsigned grid, unsigned block, void** args, const char* api) {
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, name, &f)) return rc;
+    return launch(ctx, f, grid, block, args, api);
+}
+
+int attn_dim_ok(int dim) { return dim == 64 || dim == 128; }
+
+int attn_fused(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, unsigned* counters, void* out,
+               int q_heads, int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
+               const int* pos_dev, const char* api) {
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || !attn_dim_ok(dim) || max_seq <= 0 || csz <= 0 ||
+        csz > 512 || n_chunks <= 0 || (long long)n_chunks * csz < max_seq)
+        return fail(CIMA_E_INVALID,
+                    "%s: q_heads=%d kv_heads=%d dim=%d max_seq=%d csz=%d n_chunks=%d (dim 64 or 128, q_heads a "
+                    "multiple of kv_heads, csz <= 512, n_chunks * csz >= max_seq)",
+                    api, q_heads, kv_heads, dim, max_seq, csz, n_chunks);
+    if (!qkv || !kc || !vc || !part || !counters || !out || !pos_dev)
+        return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    if (!aligned(kc, 16) || !aligned(vc, 16) || !aligned(qkv, 4))
+        return fail(CIMA_E_INVALID, "%s: misaligned cache (16 B) or qkv (4 B)", api);
+    char name[48];
+    snprintf(name, sizeof name, "cima_attn_decode_d%d", dim);
+    void* args[] = {&qkv, &kc, &vc, &part, &counters, &out, &q_heads, &kv_heads, &max_seq, &csz, &n_chunks,
+                    &theta, &scale, &pos_dev};
+    return launch_named(ctx, name, (unsigned)(q_heads * n_chunks), 256, args, api);
+}
+
+}  // namespace
+
+int cima_hip_rmsnorm(cima_hip_ctx* ctx, const void* x, const void* w, void* y, int rows, int n, float eps) {
+    if (int rc = ready(ctx, kApiRms)) return rc;
+    if (rows < 0 || n <= 0 || !(eps >= 0.f)) return fail(CIMA_E_INVALID, "%s: rows=%d n=%d eps=%g", kApiRms, rows, n, eps);
+    if (rows == 0) return 0;
+    if (!x || !y) return fail(CIMA_E_INVALID, "%s: null x or y", kApiRms);
+    void* args[] = {&x, &w, &y, &n, &eps};
+    return launch_named(ctx, "cima_rmsnorm_f16", (unsigned)rows, 256, args, kApiRms);
+}
+
+int cima_hip_rope(cima_hip_ctx* ctx, void* x, int rows, int heads, int dim, int pos0, float theta, int nfreqs,
+                  const int* pos_dev) {
+    const char* api = "cima_hip_rope";
+    if (int rc = ready(ctx, api)) return rc;
+    if (rows < 0 || heads <= 0 || dim <= 0 || dim % 2 || nfreqs < 0 || (long long)rows * heads > 0x7fffffffLL)
+        return fail(CIMA_E_INVALID, "%s: rows=%d heads=%d dim=%d nfreqs=%d", api, rows, heads, dim, nfreqs);
+    if (rows == 0) return 0;
+    if (!x) return fail(CIMA_E_INVALID, "%s: null x", api);
+    void* args[] = {&x, &heads, &dim, &pos0, &theta, &nfreqs, &pos_dev};
+    return launch_named(ctx, "cima_rope_f16", (unsigned)(rows * heads), 64, args, api);
+}
+
+int cima_hip_kv_append(cima_hip_ctx* ctx, const void* k, const void* v, void* kc, void* vc, int rows, int kv_heads,
+                       int dim, int pos, int max_seq, const int* pos_dev) {
+    const char* api = "cima_hip_kv_append";
+    if (int rc = ready(ctx, api)) return rc;
+    if (rows < 0 || kv_heads <= 0 || dim <= 0 || max_seq <= 0)
+        return fail(CIMA_E_INVALID, "%s: rows=%d kv_heads=%d dim=%d max_seq=%d", api, rows, kv_heads, dim, max_seq);
+    if (rows == 0) return 0;
+    if (!k || !v || !kc || !vc) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    void* args[] = {&k, &v, &kc, &vc, &kv_heads, &dim, &pos, &max_seq, &pos_dev};
+    return launch_named(ctx, "cima_kv_append_f16", (unsigned)rows, 256, args, api);
+}
+
+int cima_hip_attn_decode_split(cima_hip_ctx* ctx, const void* q, const void* kc, const void* vc, float* part,
+                               int q_heads, int kv_heads, int dim, int seq, int max_seq, int csz, int n_chunks,
+                               float scale, int window, const int* pos_dev) {
+    const char* api = "cima_hip_attn_decode_split";
+    if (int rc = ready(ctx, api)) return rc;
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || !attn_dim_ok(dim) || max_seq <= 0 || csz <= 0 ||
+        csz > 512 || n_chunks <= 0 || (long long)n_chunks * csz < max_seq || seq < 0 || window < 0)
+        return fail(CIMA_E_INVALID, "%s: q_heads=%d kv_heads=%d dim=%d seq=%d max_seq=%d csz=%d n_chunks=%d", api,
+                    q_heads, kv_heads, dim, seq, max_seq, csz, n_chunks);
+    if (!q || !kc || !vc || !part) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    if (!aligned(kc, 16) || !aligned(vc, 16)) return fail(CIMA_E_INVALID, "%s: cache must be 16-byte aligned", api);
+    char name[48];
+    snprintf(name, sizeof name, "cima_attn_split_d%d", dim);
+    void* args[] = {&q, &kc, &vc, &part, &q_heads, &kv_heads, &seq, &max_seq, &csz, &n_chunks, &scale, &window, &pos_dev};
+    return launch_named(ctx, name, (unsigned)(q_heads * n_chunks), 256, args, api);
+}
+
+int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_heads, int dim, int csz, int n_chunks,
+                         int seq, int max_seq, int window, const int* pos_dev) {
+    const char* api = "cima_hip_attn_reduce";
+    if (int rc = ready(ctx, api)) return rc;
+    if (q_heads <= 0 || !attn_dim_ok(dim) || csz <= 0 || n_chunks <= 0 || seq < 0 || max_seq <= 0 || window < 0)
+        return fail(CIMA_E_INVALID, "%s: q_heads=%d dim=%d csz=%d n_chunks=%d seq=%d", api, q_heads, dim, csz,
+                    n_chunks, seq);
+    if (!part || !out) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    char name[48];
+    snprintf(name, sizeof name, "cima_attn_reduce_d%d", dim);
+    void* args[] = {&part, &out, &csz, &n_chunks, &seq, &max_seq, &window, &pos_dev};
+    return launch_named(ctx, name, (unsigned)q_heads, 256, args, api);
+}
+
+int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, unsigned* counters,
+                         void* out, int q_heads, int kv_heads, int dim, int max_seq, int csz, int n_chunks,
+                         float theta, float scale, const int* pos_dev) {
+    const char* api = "cima_hip_attn_decode";
+    if (int rc = ready(ctx, api)) return rc;
+    return attn_fused(ctx, qkv, kc, vc, part, counters, out, q_heads, kv_heads, dim, max_seq, csz, n_chunks, theta,
+                      scale, pos_dev, api);
+}
+
+int cima_hip_argmax(cima_hip_ctx* ctx, const void* x, unsigned long long* slot, int n, float cap) {
+    const char* api = "cima_hip_argmax";
+    if (int rc = ready(ctx, api)) return rc;
+    if (n <= 0 || !x || !slot || !aligned(slot, 8)) return fail(CIMA_E_INVALID, "%s: n=%d or null/misaligned pointer", api, n);
+    unsigned grid = (unsigned)((n + 255) / 256);
+    if (grid > 1024) grid = 1024;
+    void* args[] = {&x, &slot, &n, &cap};
+    return launch_named(ctx, "cima_argmax_f16", grid, 256, args, api);
+}
+
+int cima_hip_argmax_to_ids(cima_hip_ctx* ctx, unsigned long long* slot, unsigned int* ids, int* pos_dev) {
+    const char* api = "cima_hip_argmax_to_ids";
+    if (int rc = ready(ctx, api)) return rc;
+    if (!slot) return fail(CIMA_E_INVALID, "%s: null slot", api);
+    void* args[] = {&slot, &ids, &pos_dev};
+    return launch_named(ctx, "cima_argmax_to_ids", 1, 64, args, api);
+}
+
+int cima_hip_pos_bump(cima_hip_ctx* ctx, int* pos_dev) {
+    const char* api = "cima_hip_pos_bump";
+    if (int rc = ready(ctx, api)) return rc;
+    if (!pos_dev) return fail(CIMA_E_INVALID, "%s: null counter", api);
+    void* args[] = {&pos_dev};
+    return launch_named(ctx, "cima_pos_bump", 1, 64, args, api);
+}
+
+int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
+    const char* api = "cima_hip_decode_step";
+    if (int rc = ready(ctx, api)) return rc;
+    if (!d || !d->layers) return fail(CIMA_E_INVALID, "%s: null decoder or layer table", api);
+    const int hd = d->head_dim, qd = d->q_heads * hd, kvd = d->kv_heads * hd;
+    if (d->n_layers <= 0 || d->hidden <= 0 || d->ffn <= 0 || d->vocab <= 0 || d->q_heads <= 0 || d->kv_heads <= 0)
+        return fail(CIMA_E_INVALID, "%s: layers=%d hidden=%d ffn=%d vocab=%d heads=%d/%d", api, d->n_layers,
+                    d->hidden, d->ffn, d->vocab, d->q_heads, d->kv_heads);
+    if (!d->x || !d->qkv || !d->att || !d->act || !d->logits || !d->part || !d->counters || !d->slot || !d->ids ||
+        !d->pos || !d->embed || !d->final_norm)
+        return fail(CIMA_E_INVALID, "%s: null workspace, embedding or final norm pointer", api);
+    const int csz = d->attn_chunk > 0 ? d->attn_chunk : 128;
+    const int nch = (d->max_seq + csz - 1) / csz;
+    const float scale = 1.0f / sqrtf((float)hd);
+    const void* head = d->head ? d->head : d->embed;
+    const int head_type = d->head ? d->head_type : d->embed_type;
+    // enqueue_decode_device (src/models/transformer.rs:1440-1461)
+    if (int rc = cima_hip_gguf_gather(ctx, d->embed_type, d->embed, d->ids, d->x, 1, d->hidden)) return rc;
+    for (int l = 0; l < d->n_layers; l++) {
+        const cima_decoder_layer& L = d->layers[l];
+        // rmsnorm -> q|k|v GEMV with bias (forward_chunk_at :1030-1098)
+        if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.attn_norm, d->rms_eps, L.wqkv, L.bqkv,
+                                                d->qkv, qd + 2 * kvd, d->hidden, 0, CIMA_DT_F16))
+            return rc;
+        // rope q, k; kv append; split attention + merge (:1100-1173)
+        if (int rc = attn_fused(ctx, d->qkv, L.k_cache, L.v_cache, d->part, d->counters, d->att, d->q_heads,
+                                d->kv_heads, hd, d->max_seq, csz, nch, d->rope_theta, scale, d->pos, api))
+            return rc;
+        // o projection + residual (:1238)
+        if (int rc = cima_hip_gguf_gemv(ctx, d->ggml_type, d->att, L.wo, nullptr, d->x, d->hidden, qd, 1, CIMA_DT_F16))
+            return rc;
+        // rmsnorm -> gate|up SwiGLU -> down + residual (:1240-1260)
+        if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.ffn_norm, d->rms_eps, L.w_gate_up,
+                                                nullptr, d->act, d->ffn, d->hidden, 2, CIMA_DT_F16))
+            return rc;
+        if (int rc = cima_hip_gguf_gemv(ctx, d->ggml_type, d->act, L.w_down, nullptr, d->x, d->hidden, d->ffn, 1,
+                                        CIMA_DT_F16))
+            return rc;
+    }
+    // final norm -> head -> argmax -> ids[0], pos += 1
+    if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, head_type, d->x, d->final_norm, d->rms_eps, head, nullptr,
+                                            d->logits, d->vocab, d->hidden, 0, CIMA_DT_F16))
+        return rc;
+    if (int rc = cima_hip_argmax(ctx, d->logits, d->slot, d->vocab, 0.f)) return rc;
+    return cima_hip_argmax_to_ids(ctx, d->slot, d->ids, d->pos);
 }
 
 }  // extern "C"

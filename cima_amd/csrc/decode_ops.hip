@@ -1,0 +1,409 @@
+// Decode-step support kernels for gfx950 (CDNA4): the code object
+// cima_decode.hsaco.  These are the non-GEMV launches of one batch-1 decode
+// step of the reference's transformer family (forward_chunk_at,
+// src/models/transformer.rs:1012-1300, and enqueue_decode_device,
+// :1440-1461): RMSNorm, RoPE, the KV-cache append, split ("flash-decode")
+// attention with its log-sum-exp merge, and the greedy argmax feedback.
+//
+// Every kernel reads and writes f16 activations (the engine's activation
+// type) and computes in fp32.  The standalone kernels keep the reference's
+// argument meaning (src/kernels.cu:37-50, 244-262, 397-454, 547-639) so they
+// are drop-ins one by one; cima_attn_decode_* fuses RoPE, the KV append, the
+// per-chunk attention and the merge of one layer into a single launch.
+#include "gguf_formats.h"
+
+// |v| clamped to 65000 (g_sat16, src/kernels.cu:30-35)
+DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
+
+DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+
+// y[row] = f16(sat(x) * rsqrt(mean(sat(x)^2) + eps) * w); w may be null
+// (unit weight).  One 256-thread workgroup per row (k_rmsnorm,
+// src/kernels.cu:37-50).
+extern "C" __global__ __launch_bounds__(256) void cima_rmsnorm_f16(const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ w,
+                                                                   uint16_t* __restrict__ y, int n, float eps) {
+    __shared__ float red[4];
+    const uint16_t* xr = x + (size_t)blockIdx.x * n;
+    uint16_t* yr = y + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float v = sat16(h2f(xr[i]));
+        ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float g = w ? h2f(w[i]) : 1.0f;
+        yr[i] = (uint16_t)f2h(sat16(h2f(xr[i])) * inv * g);
+    }
+}
+
+// --------------------------------------------------------------------- RoPE
+
+// NeoX half-split rotation of pair i (elements i and i + dim/2) at position
+// p: frequency theta^(-2i/dim) (k_rope, src/kernels.cu:397-414).
+DEV void rope_rot(float a, float b, float p, int i, int dim, float theta, float& oa, float& ob) {
+    const float freq = powf(theta, -2.0f * (float)i / (float)dim);
+    float s, c;
+    sincosf(p * freq, &s, &c);
+    oa = a * c - b * s;
+    ob = a * s + b * c;
+}
+
+// In place over x [rows, heads, dim]: row r sits at position pos0 + r, or
+// *pos_dev + r when pos_dev is set (graph replay).  Pairs i >= nfreqs pass
+// through.  Grid rows * heads, 64 threads striding the dim/2 pairs.
+extern "C" __global__ __launch_bounds__(64) void cima_rope_f16(uint16_t* __restrict__ x, int heads, int dim,
+                                                               int pos0, float theta, int nfreqs,
+                                                               const int* __restrict__ pos_dev) {
+    const int row = blockIdx.x / heads, h = blockIdx.x % heads;
+    if (pos_dev) pos0 = *pos_dev;
+    uint16_t* v = x + ((size_t)row * heads + h) * dim;
+    const float p = (float)(pos0 + row);
+    const int half = dim >> 1;
+    for (int i = threadIdx.x; i < half && i < nfreqs; i += 64) {
+        float oa, ob;
+        rope_rot(h2f(v[i]), h2f(v[i + half]), p, i, dim, theta, oa, ob);
+        v[i] = (uint16_t)f2h(oa);
+        v[i + half] = (uint16_t)f2h(ob);
+    }
+}
+
+// ---------------------------------------------------------------- KV append
+
+// Rows r of k, v [rows, kv_heads*dim] go to cache [kv_heads, max_seq, dim]
+// at position pos + r (or *pos_dev + r); positions >= max_seq are dropped
+// rather than written out of bounds (k_kv_append, src/kernels.cu:440-454).
+extern "C" __global__ __launch_bounds__(256) void cima_kv_append_f16(const uint16_t* __restrict__ k,
+                                                                     const uint16_t* __restrict__ v,
+                                                                     uint16_t* __restrict__ kc,
+                                                                     uint16_t* __restrict__ vc, int kv_heads,
+                                                                     int dim, int pos, int max_seq,
+                                                                     const int* __restrict__ pos_dev) {
+    const int row = blockIdx.x;
+    if (pos_dev) pos = *pos_dev;
+    const int at = pos + row;
+    if (at < 0 || at >= max_seq) return;
+    const int n = kv_heads * dim;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const int h = i / dim, d = i % dim;
+        const size_t idx = ((size_t)h * max_seq + at) * dim + d;
+        kc[idx] = k[(size_t)row * n + i];
+        vc[idx] = v[(size_t)row * n + i];
+    }
+}
+
+// ---------------------------------------------------------------- attention
+//
+// Partials: part[(head * n_chunks + chunk) * (D + 2)] = {m, l, acc[D]} with m
+// the chunk's maximum score, l = sum exp(score - m), acc = sum exp(score -
+// m) * v -- the reference's layout (src/kernels.cu:547-610), so the split
+// and merge kernels below interoperate with it.
+
+constexpr int ATT_MAX_CSZ = 512;
+
+template <int D>
+struct AttnLds {
+    float q[D];
+    float kn[D];
+    float vn[D];
+    float p[ATT_MAX_CSZ];
+    float red[8];
+    float acc[512 / D][D];  // one accumulator row per position group
+    int last;
+};
+
+// One chunk [s0, s1) of one query head against the cache rows kh / vh
+// ([max_seq, D] f16).  Position `snew` (if in the chunk) takes its key and
+// value from L.kn / L.vn.  256 threads: scores one position per thread,
+// then lane pairs of dims x position groups for the weighted value sum.
+// Writes {m, l, acc} to `dst`.
+template <int D>
+DEV void attn_chunk(AttnLds<D>& L, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh, int s0,
+                    int s1, int snew, float scale, float* __restrict__ dst) {
+    const int t = threadIdx.x, len = s1 - s0;
+    float mloc = -INFINITY;
+    for (int j = t; j < len; j += 256) {
+        const int s = s0 + j;
+        float d = 0.f;
+        if (s == snew) {
+#pragma unroll
+            for (int e = 0; e < D; e++) d += L.q[e] * L.kn[e];
+        } else {
+            const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)s * D);
+#pragma unroll
+            for (int c = 0; c < D / 8; c++) {
+                const uint4 u = kr[c];
+                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    d += L.q[8 * c + 2 * e] * h2f(w[e] & 0xffffu);
+                    d += L.q[8 * c + 2 * e + 1] * h2f(w[e] >> 16);
+                }
+            }
+        }
+        const float sc = d * scale;
+        L.p[j] = sc;
+        mloc = fmaxf(mloc, sc);
+    }
+    mloc = wave_max(mloc);
+    if ((t & 63) == 0) L.red[t >> 6] = mloc;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(L.red[0], L.red[1]), fmaxf(L.red[2], L.red[3]));
+    float lsum = 0.f;
+    for (int j = t; j < len; j += 256) {
+        const float e = __expf(L.p[j] - M);
+        L.p[j] = e;
+        lsum += e;
+    }
+    lsum = wave_sum(lsum);
+    if ((t & 63) == 0) L.red[4 + (t >> 6)] = lsum;
+    __syncthreads();
+    // weighted value sum: lane pair dp owns dims 2dp, 2dp+1; G groups
+    // stride the positions
+    constexpr int G = 512 / D;
+    const int dp = t % (D / 2), g = t / (D / 2);
+    float a0 = 0.f, a1 = 0.f;
+    for (int j = g; j < len; j += G) {
+        const int s = s0 + j;
+        const float pj = L.p[j];
+        float v0, v1;
+        if (s == snew) {
+            v0 = L.vn[2 * dp];
+            v1 = L.vn[2 * dp + 1];
+        } else {
+            const uint32_t u = reinterpret_cast<const uint32_t*>(vh + (size_t)s * D)[dp];
+            v0 = h2f(u & 0xffffu);
+            v1 = h2f(u >> 16);
+        }
+        a0 += pj * v0;
+        a1 += pj * v1;
+    }
+    L.acc[g][2 * dp] = a0;
+    L.acc[g][2 * dp + 1] = a1;
+    __syncthreads();
+    if (t < D) {
+        float a = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < G; gg++) a += L.acc[gg][t];
+        dst[2 + t] = a;
+    }
+    if (t == 0) {
+        dst[0] = M;
+        dst[1] = (L.red[4] + L.red[5]) + (L.red[6] + L.red[7]);
+    }
+}
+
+// Merge chunks [c0, active) of one head: out = sum_c e^(m_c - M) acc_c /
+// sum_c e^(m_c - M) l_c (k_attn_reduce, src/kernels.cu:614-639).  Threads
+// t < D each produce one output element.
+template <int D>
+DEV void attn_merge(const float* __restrict__ ph, int c0, int active, uint16_t* __restrict__ oh) {
+    const int t = threadIdx.x;
+    if (t >= D) return;
+    float M = -INFINITY;
+    for (int c = c0; c < active; c++) M = fmaxf(M, ph[(size_t)c * (D + 2)]);
+    float Ls = 0.f, a = 0.f;
+    for (int c = c0; c < active; c++) {
+        const float* pc = ph + (size_t)c * (D + 2);
+        const float w = __expf(pc[0] - M);
+        Ls += w * pc[1];
+        a += w * pc[2 + t];
+    }
+    oh[t] = (uint16_t)f2h(a / Ls);
+}
+
+// Live length and first position of the attention window: seq = *pos_dev +
+// 1 when pos_dev is set, capped at max_seq; window > 0 keeps the last
+// `window` positions.
+DEV void attn_range(int& seq, int max_seq, int window, const int* pos_dev, int& wlo) {
+    if (pos_dev) seq = *pos_dev + 1;
+    seq = min(seq, max_seq);
+    wlo = (window > 0 && seq > window) ? seq - window : 0;
+}
+
+// Split decode attention (k_attn_decode_split, src/kernels.cu:547-610): one
+// workgroup per (query head, chunk of csz positions); q [q_heads, D] f16
+// already rotated; GQA maps head h to kv head h / (q_heads / kv_heads).
+// Chunks past the live length write nothing.
+template <int D>
+DEV void attn_split_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+                         const uint16_t* __restrict__ vc, float* __restrict__ part, int q_heads, int kv_heads,
+                         int seq, int max_seq, int csz, int n_chunks, float scale, int window,
+                         const int* __restrict__ pos_dev) {
+    __shared__ AttnLds<D> L;
+    int wlo;
+    attn_range(seq, max_seq, window, pos_dev, wlo);
+    const int h = blockIdx.x / n_chunks, ci = blockIdx.x % n_chunks;
+    const int s0 = max(ci * csz, wlo), s1 = min(ci * csz + csz, seq);
+    if (s0 >= s1) return;
+    const int kvh = h / (q_heads / kv_heads);
+    if (threadIdx.x < D) L.q[threadIdx.x] = h2f(q[(size_t)h * D + threadIdx.x]);
+    __syncthreads();
+    attn_chunk<D>(L, kc + (size_t)kvh * max_seq * D, vc + (size_t)kvh * max_seq * D, s0, s1, -1, scale,
+                  part + ((size_t)h * n_chunks + ci) * (D + 2));
+}
+
+template <int D>
+DEV void attn_reduce_body(const float* __restrict__ part, uint16_t* __restrict__ out, int csz, int n_chunks,
+                          int seq, int max_seq, int window, const int* __restrict__ pos_dev) {
+    int wlo;
+    attn_range(seq, max_seq, window, pos_dev, wlo);
+    const int h = blockIdx.x;
+    const int active = min((seq + csz - 1) / csz, n_chunks);
+    attn_merge<D>(part + (size_t)h * n_chunks * (D + 2), wlo / csz, active, out + (size_t)h * D);
+}
+
+// Fused decode attention of one layer at position pos = *pos_dev:
+//   qkv = [q (q_heads*D) | k (kv_heads*D) | v (kv_heads*D)] f16, the output
+//   of the fused q/k/v GEMV (biases applied, RoPE not yet);
+//   every workgroup (query head h, chunk ci) rotates its q; the chunk that
+//   holds pos also rotates the new k, takes the new k and v from registers
+//   for position pos, and (first head of each kv group) appends them to the
+//   cache; the chunk's partial goes to `part`; the last workgroup of head h
+//   to finish (an agent-scope counter per head, counters[h], left at 0 for
+//   the next launch) merges the head's partials into out [q_heads, D].
+// Replaces k_rope x2 + k_kv_append + k_attn_decode_split + k_attn_reduce
+// (src/models/transformer.rs:1100-1173).  counters must hold zeros before
+// the first launch; `part` holds q_heads * n_chunks * (D + 2) floats.
+template <int D>
+DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                         float* __restrict__ part, unsigned* __restrict__ counters, uint16_t* __restrict__ out,
+                         int q_heads, int kv_heads, int max_seq, int csz, int n_chunks, float theta, float scale,
+                         const int* __restrict__ pos_dev) {
+    __shared__ AttnLds<D> L;
+    const int t = threadIdx.x;
+    const int pos = *pos_dev;
+    const int seq = min(pos + 1, max_seq);
+    const int h = blockIdx.x / n_chunks, ci = blockIdx.x % n_chunks;
+    const int grp = q_heads / kv_heads, kvh = h / grp;
+    const int s0 = ci * csz, s1 = min(s0 + csz, seq);
+    const bool has_new = pos < max_seq && s0 <= pos && pos < s1;
+    float* dst = part + ((size_t)h * n_chunks + ci) * (D + 2);
+    uint16_t* kh = kc + (size_t)kvh * max_seq * D;
+    uint16_t* vh = vc + (size_t)kvh * max_seq * D;
+    if (s0 < s1) {
+        const float p = (float)pos;
+        if (t < D / 2) {
+            const uint16_t* qh = qkv + (size_t)h * D;
+            float oa, ob;
+            rope_rot(h2f(qh[t]), h2f(qh[t + D / 2]), p, t, D, theta, oa, ob);
+            L.q[t] = h2f(f2h(oa));
+            L.q[t + D / 2] = h2f(f2h(ob));
+        } else if (has_new && t < D) {
+            const int i = t - D / 2;
+            const uint16_t* kn = qkv + (size_t)q_heads * D + (size_t)kvh * D;
+            float oa, ob;
+            rope_rot(h2f(kn[i]), h2f(kn[i + D / 2]), p, i, D, theta, oa, ob);
+            const uint32_t ha = f2h(oa), hb = f2h(ob);
+            L.kn[i] = h2f(ha);
+            L.kn[i + D / 2] = h2f(hb);
+            if (h % grp == 0) {
+                kh[(size_t)pos * D + i] = (uint16_t)ha;
+                kh[(size_t)pos * D + i + D / 2] = (uint16_t)hb;
+            }
+        } else if (has_new && t >= D && t < 2 * D) {
+            const int i = t - D;
+            const uint16_t vv = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + i];
+            L.vn[i] = h2f(vv);
+            if (h % grp == 0) vh[(size_t)pos * D + i] = vv;
+        }
+        __syncthreads();
+        attn_chunk<D>(L, kh, vh, s0, s1, has_new ? pos : -1, scale, dst);
+    }
+    // publish this chunk's partial, then count it; the last arrival merges
+    __threadfence();
+    __syncthreads();
+    if (t == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        L.last = prev == (unsigned)(n_chunks - 1);
+    }
+    __syncthreads();
+    if (!L.last) return;
+    __threadfence();
+    const int active = min((seq + csz - 1) / csz, n_chunks);
+    attn_merge<D>(part + (size_t)h * n_chunks * (D + 2), 0, active, out + (size_t)h * D);
+    if (t == 0) __hip_atomic_store(&counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+#define ATTN_KERNELS(D)                                                                                          \
+    extern "C" __global__ __launch_bounds__(256) void cima_attn_split_d##D(                                      \
+        const uint16_t* q, const uint16_t* kc, const uint16_t* vc, float* part, int q_heads, int kv_heads,       \
+        int seq, int max_seq, int csz, int n_chunks, float scale, int window, const int* pos_dev) {              \
+        attn_split_body<D>(q, kc, vc, part, q_heads, kv_heads, seq, max_seq, csz, n_chunks, scale, window,       \
+                           pos_dev);                                                                             \
+    }                                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void cima_attn_reduce_d##D(                                     \
+        const float* part, uint16_t* out, int csz, int n_chunks, int seq, int max_seq, int window,               \
+        const int* pos_dev) {                                                                                    \
+        attn_reduce_body<D>(part, out, csz, n_chunks, seq, max_seq, window, pos_dev);                            \
+    }                                                                                                            \
+    extern "C" __global__ __launch_bounds__(256) void cima_attn_decode_d##D(                                     \
+        const uint16_t* qkv, uint16_t* kc, uint16_t* vc, float* part, unsigned* counters, uint16_t* out,         \
+        int q_heads, int kv_heads, int max_seq, int csz, int n_chunks, float theta, float scale,                 \
+        const int* pos_dev) {                                                                                    \
+        attn_fused_body<D>(qkv, kc, vc, part, counters, out, q_heads, kv_heads, max_seq, csz, n_chunks, theta,   \
+                           scale, pos_dev);                                                                      \
+    }
+
+ATTN_KERNELS(64)
+ATTN_KERNELS(128)
+
+// ------------------------------------------------------------ greedy argmax
+
+// slot = max over i of (orderable(f32 bits of v_i) << 32 | i), v_i = x_i or
+// cap * tanh(x_i / cap) when cap > 0: one u64 atomic max per workgroup
+// resolves value and index together, ties going to the higher index
+// (k_argmax_softcap, src/kernels.cu:244-262).  slot must hold 0 on entry.
+DEV unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
+extern "C" __global__ __launch_bounds__(256) void cima_argmax_f16(const uint16_t* __restrict__ x,
+                                                                  unsigned long long* __restrict__ slot, int n,
+                                                                  float cap) {
+    __shared__ unsigned long long red[4];
+    unsigned long long best = 0ull;
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        float v = h2f(x[i]);
+        if (cap > 0.f) v = cap * tanhf(v / cap);
+        uint32_t b = __builtin_bit_cast(uint32_t, v);
+        b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+        best = umax64(best, ((unsigned long long)b << 32) | (uint32_t)i);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)best, o), hi = __shfl_xor((uint32_t)(best >> 32), o);
+        best = umax64(best, ((unsigned long long)hi << 32) | lo);
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) atomicMax(slot, umax64(umax64(red[0], red[1]), umax64(red[2], red[3])));
+}
+
+// ids[0] = index held in slot; slot back to 0 for the next argmax; and, if
+// pos_dev is set, *pos_dev += 1 (k_argmax_extract + k_pos_bump,
+// src/kernels.cu:309-318).
+extern "C" __global__ void cima_argmax_to_ids(unsigned long long* __restrict__ slot, unsigned* __restrict__ ids,
+                                              int* __restrict__ pos_dev) {
+    if (blockIdx.x != 0 || threadIdx.x != 0) return;
+    if (ids) ids[0] = (unsigned)(*slot);
+    *slot = 0ull;
+    if (pos_dev) *pos_dev += 1;
+}
+
+extern "C" __global__ void cima_pos_bump(int* __restrict__ pos_dev) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *pos_dev += 1;
+}

@@ -208,36 +208,85 @@ constexpr int xstage_bytes(int k) { return 2 * k + 16 * (k >> PADSH) + 4 * (k >>
 // x -> LDS: thread t takes 16-element chunks t, t+256, ...; the two chunks
 // of a 32-element block sit in neighbouring lanes, which exchange their
 // |x| maxima with one DPP quad permute.
+template <int ACT>
+DEV void load16(const void* __restrict__ x, int c, float v[16]) {
+    if constexpr (ACT == ACT_F32) {
+        const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 16 * c);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float4 t = p[i];
+            v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+        }
+    } else {
+        const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + 16 * c);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            uint4 t = p[i];
+            const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                v[8 * i + 2 * j] = h2f(w[j] & 0xffffu);
+                v[8 * i + 2 * j + 1] = h2f(w[j] >> 16);
+            }
+        }
+    }
+}
+
+// |v| clamped to 65000 (k_rmsnorm's g_sat16, src/kernels.cu:30-35); NaN
+// becomes a finite value as with CUDA's fminf/fmaxf
+DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
+
+// Optional RMSNorm prologue (k_rmsnorm, src/kernels.cu:37-50): with norm_w
+// set, the GEMV multiplies W by h = f16(sat(x) * rsqrt(mean(sat(x)^2) + eps)
+// * norm_w) instead of x -- h is rounded to f16 (f32 activations: kept in
+// fp32) as the reference's separate rmsnorm launch writes it.
+template <int ACT>
+DEV float norm_scale(const void* __restrict__ x, int k, float eps) {
+    __shared__ float red[4];
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < (k >> 4); c += 256) {
+        float v[16];
+        load16<ACT>(x, c, v);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float s = sat16(v[i]);
+            ss += s * s;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    return 1.0f / sqrtf(tot / (float)k + eps);
+}
+
+// x -> LDS: thread t takes 16-element chunks t, t+256, ...; the two chunks
+// of a 32-element block sit in neighbouring lanes, which exchange their
+// |x| maxima with one DPP quad permute.
 template <int ACT, int PADSH>
-DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, float* xsum) {
+DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, float* xsum,
+                 const void* __restrict__ norm_w, float eps) {
     const int nchunks = k >> 4;
+    const float inv = norm_w ? norm_scale<ACT>(x, k, eps) : 1.f;
     for (int c = threadIdx.x; c < nchunks; c += 256) {
         float v[16];
-        if constexpr (ACT == ACT_F32) {
-            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + 16 * c);
+        load16<ACT>(x, c, v);
+        if (norm_w) {
+            float g[16];
+            load16<ACT>(norm_w, c, g);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float4 t = p[i];
-                v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
-            }
-        } else {
-            const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + 16 * c);
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                uint4 t = p[i];
-                const uint32_t w[4] = {t.x, t.y, t.z, t.w};
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    v[8 * i + 2 * j] = h2f(w[j] & 0xffffu);
-                    v[8 * i + 2 * j + 1] = h2f(w[j] >> 16);
-                }
+            for (int i = 0; i < 16; i++) {
+                const float h = sat16(v[i]) * inv * g[i];
+                if constexpr (ACT == ACT_F32) v[i] = h;
+                else v[i] = h2f(f2h(h));
             }
         }
         float amax = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
         amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0xB1, 0xf, 0xf, false)));
-        const float inv = amax > 0.f ? 32639.f / amax : 0.f;
+        const float qinv = amax > 0.f ? 32639.f / amax : 0.f;
         const float scale = amax * (1.0f / 32639.f);
         uint32_t hw[4], lw[4];
         int qsum = 0;
@@ -246,7 +295,7 @@ DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, floa
             uint32_t hv = 0, lv = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int q = (int)__builtin_rintf(v[4 * i + j] * inv);
+                const int q = (int)__builtin_rintf(v[4 * i + j] * qinv);
                 const int hi = (q + 128) >> 8;
                 const int lo = q - (hi << 8);
                 hv |= (uint32_t)(hi & 0xff) << (8 * j);
@@ -292,7 +341,7 @@ template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI>
 __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ wa,
                           const uint8_t* __restrict__ wb, const void* __restrict__ bias_a,
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
-                          int mode, int lpr_shift) {
+                          int mode, int lpr_shift, const void* __restrict__ norm_w, float eps) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int S = PAIR ? 2 * R : R;  // weight row streams per lane
     uint8_t* xq = lds;
@@ -361,7 +410,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     Slot bufA, bufB;
     issue(bufA, 0);
     // the first row group is in flight while x is staged
-    stage_x<ACT, F::PADSH>(x, k, xq, xs, xsum);
+    stage_x<ACT, F::PADSH>(x, k, xq, xs, xsum, norm_w, eps);
 
     typename F::Xf xreg;
     if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
@@ -427,8 +476,10 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #define GEMV_KERNEL(NAME, F, R, IT, ACT, PAIR, EPI)                                              \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         const void* x, const uint8_t* wa, const uint8_t* wb, const void* bias_a,                  \
-        const void* bias_b, void* y, int n, int k, int mode, int lpr_shift) {                     \
-        gemv_body<F, R, IT, ACT, PAIR, EPI>(x, wa, wb, bias_a, bias_b, y, n, k, mode, lpr_shift); \
+        const void* bias_b, void* y, int n, int k, int mode, int lpr_shift, const void* norm_w,   \
+        float eps) {                                                                              \
+        gemv_body<F, R, IT, ACT, PAIR, EPI>(x, wa, wb, bias_a, bias_b, y, n, k, mode, lpr_shift,   \
+                                            norm_w, eps);                                         \
     }
 
 // name: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair][_epi]

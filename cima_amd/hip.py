@@ -24,16 +24,36 @@ from . import gguf
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 LIBHIP = os.path.join(LIB_DIR, "libcima_hip.so")
-CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco") for n in ("gemv", "gemm", "dequant")]
+CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco") for n in ("gemv", "gemm", "dequant", "decode")]
 
 # declared in include/cima_hip.h, in order
 EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
     "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
-    "cima_hip_gguf_gemv",
+    "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
+    "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
+    "cima_hip_attn_decode", "cima_hip_argmax", "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
 )
+
+
+class DecoderLayer(ctypes.Structure):
+    """``cima_decoder_layer`` (include/cima_hip.h)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "attn_norm", "wqkv", "bqkv", "wo", "ffn_norm", "w_gate_up", "w_down", "k_cache", "v_cache")]
+
+
+class Decoder(ctypes.Structure):
+    """``cima_decoder`` (include/cima_hip.h)."""
+    _fields_ = ([(n, ctypes.c_int) for n in (
+        "ggml_type", "embed_type", "head_type", "n_layers", "hidden", "q_heads", "kv_heads", "head_dim", "ffn",
+        "vocab", "max_seq", "attn_chunk")]
+        + [("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+        + [(n, ctypes.c_void_p) for n in ("embed", "head", "final_norm")]
+        + [("layers", ctypes.POINTER(DecoderLayer))]
+        + [(n, ctypes.c_void_p) for n in (
+            "x", "qkv", "att", "act", "logits", "part", "counters", "slot", "ids", "pos")])
 
 E_INVALID, E_FORMAT, E_NO_KERNEL, E_NOT_INIT = -1, -2, -3, -4
 
@@ -73,6 +93,18 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_set_gemv_grid.argtypes = [P, I]
     L.cima_hip_set_gemm_tile.argtypes = [P, I]
     L.cima_hip_gguf_gemv.argtypes = [P, I, P, P, P, P, I, I, I, I]
+    F = ctypes.c_float
+    L.cima_hip_rmsnorm_gguf_gemv.argtypes = [P, I, P, P, F, P, P, P, I, I, I, I]
+    L.cima_hip_rmsnorm.argtypes = [P, P, P, P, I, I, F]
+    L.cima_hip_rope.argtypes = [P, P, I, I, I, I, F, I, P]
+    L.cima_hip_kv_append.argtypes = [P, P, P, P, P, I, I, I, I, I, P]
+    L.cima_hip_attn_decode_split.argtypes = [P, P, P, P, P, I, I, I, I, I, I, I, F, I, P]
+    L.cima_hip_attn_reduce.argtypes = [P, P, P, I, I, I, I, I, I, I, P]
+    L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, I, F, F, P]
+    L.cima_hip_argmax.argtypes = [P, P, P, I, F]
+    L.cima_hip_argmax_to_ids.argtypes = [P, P, P, P]
+    L.cima_hip_pos_bump.argtypes = [P, P]
+    L.cima_hip_decode_step.argtypes = [P, ctypes.POINTER(Decoder)]
     L.cima_hip_gguf_gemv_swiglu.argtypes = [P, I, P, P, P, P, P, P, I, I, I]
     L.cima_hip_gguf_gemm.argtypes = [P, I, P, P, P, I, I, I, I, I, I]
     L.cima_hip_gguf_dequant.argtypes = [P, I, P, P, LL]
@@ -207,3 +239,62 @@ class HipCtx:
         """``out[i,:] = dequant(table[ids[i]])`` as f16."""
         self._check(self.lib.cima_hip_gguf_gather(self.handle, int(fmt), _ptr(table), _ptr(ids), _ptr(out),
                                                   n, hidden))
+
+    def rmsnorm_gguf_gemv(self, fmt: int, x, norm_w, eps: float, w, bias, y, n: int, k: int, mode: int = 0,
+                          act_dtype: Optional[int] = None) -> None:
+        """``gguf_gemv`` of ``rmsnorm(x) * norm_w`` (the norm is never written out)."""
+        if act_dtype is None:
+            act_dtype = _act_of(x) if hasattr(x, "dtype") else gguf.DT_F32
+        self._check(self.lib.cima_hip_rmsnorm_gguf_gemv(self.handle, int(fmt), _ptr(x), _ptr(norm_w), eps, _ptr(w),
+                                                        _ptr(bias), _ptr(y), n, k, mode, act_dtype))
+
+    # -- decode-step support (f16) ------------------------------------------
+    def rmsnorm(self, x, w, y, rows: int, n: int, eps: float) -> None:
+        """CudaCtx::rmsnorm (src/cuda.rs:1180)."""
+        self._check(self.lib.cima_hip_rmsnorm(self.handle, _ptr(x), _ptr(w), _ptr(y), rows, n, eps))
+
+    def rope(self, x, rows: int, heads: int, dim: int, pos0: int, theta: float, nfreqs: int, pos_dev=None) -> None:
+        """CudaCtx::rope (src/cuda.rs:1302), in place."""
+        self._check(self.lib.cima_hip_rope(self.handle, _ptr(x), rows, heads, dim, pos0, theta, nfreqs,
+                                           _ptr(pos_dev)))
+
+    def kv_append(self, k, v, kc, vc, rows: int, kv_heads: int, dim: int, pos: int, max_seq: int,
+                  pos_dev=None) -> None:
+        """CudaCtx::kv_append (src/cuda.rs:1344)."""
+        self._check(self.lib.cima_hip_kv_append(self.handle, _ptr(k), _ptr(v), _ptr(kc), _ptr(vc), rows, kv_heads,
+                                                dim, pos, max_seq, _ptr(pos_dev)))
+
+    def attn_decode_split(self, q, kc, vc, part, q_heads: int, kv_heads: int, dim: int, seq: int, max_seq: int,
+                          csz: int, n_chunks: int, scale: float, window: int = 0, pos_dev=None) -> None:
+        """CudaCtx::attn_decode_split (src/cuda.rs:1418)."""
+        self._check(self.lib.cima_hip_attn_decode_split(self.handle, _ptr(q), _ptr(kc), _ptr(vc), _ptr(part),
+                                                        q_heads, kv_heads, dim, seq, max_seq, csz, n_chunks, scale,
+                                                        window, _ptr(pos_dev)))
+
+    def attn_reduce(self, part, out, q_heads: int, dim: int, csz: int, n_chunks: int, seq: int, max_seq: int,
+                    window: int = 0, pos_dev=None) -> None:
+        """CudaCtx::attn_reduce (src/cuda.rs:1476)."""
+        self._check(self.lib.cima_hip_attn_reduce(self.handle, _ptr(part), _ptr(out), q_heads, dim, csz, n_chunks,
+                                                  seq, max_seq, window, _ptr(pos_dev)))
+
+    def attn_decode(self, qkv, kc, vc, part, counters, out, q_heads: int, kv_heads: int, dim: int, max_seq: int,
+                    csz: int, n_chunks: int, theta: float, scale: float, pos_dev) -> None:
+        """RoPE + KV append + split attention + merge in one launch."""
+        self._check(self.lib.cima_hip_attn_decode(self.handle, _ptr(qkv), _ptr(kc), _ptr(vc), _ptr(part),
+                                                  _ptr(counters), _ptr(out), q_heads, kv_heads, dim, max_seq, csz,
+                                                  n_chunks, theta, scale, _ptr(pos_dev)))
+
+    def argmax(self, x, slot, n: int, cap: float = 0.0) -> None:
+        """CudaCtx::argmax_softcap_enqueue (src/cuda.rs:2036); slot must be 0."""
+        self._check(self.lib.cima_hip_argmax(self.handle, _ptr(x), _ptr(slot), n, cap))
+
+    def argmax_to_ids(self, slot, ids, pos_dev=None) -> None:
+        """CudaCtx::argmax_to_ids (+ pos_bump when pos_dev is given); clears slot."""
+        self._check(self.lib.cima_hip_argmax_to_ids(self.handle, _ptr(slot), _ptr(ids), _ptr(pos_dev)))
+
+    def pos_bump(self, pos_dev) -> None:
+        self._check(self.lib.cima_hip_pos_bump(self.handle, _ptr(pos_dev)))
+
+    def decode_step(self, desc: "Decoder") -> None:
+        """One greedy decode step of a whole decoder (cima_hip_decode_step)."""
+        self._check(self.lib.cima_hip_decode_step(self.handle, ctypes.byref(desc)))

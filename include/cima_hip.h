@@ -47,7 +47,8 @@ typedef struct cima_hip_ctx cima_hip_ctx;
 
 /* Context creation: replaces CudaCtx::init (src/cuda.rs:691-908) -- device
  * selection, one non-blocking stream, then loading the prebuilt gfx950 code
- * objects (cima_gemv.hsaco, cima_gemm.hsaco, cima_dequant.hsaco) with
+ * objects (cima_gemv.hsaco, cima_gemm.hsaco, cima_dequant.hsaco,
+ * cima_decode.hsaco) with
  * hipModuleLoad and resolving every kernel (the reference JIT-compiles with
  * NVRTC and resolves its KernelSet, src/cuda.rs:808-877).
  * code_dir: directory holding the code objects, or NULL for the directory
@@ -113,6 +114,16 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
 int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w,
                        const void* bias, void* y, int n, int k, int mode, int act_dtype);
 
+/* RMSNorm fused into the GEMV: the same as cima_hip_gguf_gemv (modes 0, 1,
+ * 2) applied to h = rmsnorm(x) = f16(sat(x) * rsqrt(mean(sat(x)^2) + eps) *
+ * norm_w) (f32 activations: h stays fp32), where sat clamps to +-65000.
+ * Replaces CudaCtx::rmsnorm (src/cuda.rs:1180-1198, k_rmsnorm
+ * src/kernels.cu:37-50) followed by gguf_gemv on its output, as
+ * forward_chunk_at runs them (src/models/transformer.rs:1030-1060, 1240-1252)
+ * -- h is never written to memory.  norm_w has k entries of act_dtype,
+ * 16-byte aligned. */
+int cima_hip_rmsnorm_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* norm_w, float eps,
+                               const void* w, const void* bias, void* y, int n, int k, int mode, int act_dtype);
 /* Fused gate+up SwiGLU GEMV over two separately stored weights (the
  * reference runs gate GEMV, up GEMV and k_swiglu, src/models/
  * transformer.rs:1249-1252): y = silu(Wg.x + bg) * (Wu.x + bu).
@@ -143,6 +154,112 @@ int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int ggml_type, const void* src, voi
  * ids are u32 row indices; they are not range-checked on the device. */
 int cima_hip_gguf_gather(cima_hip_ctx* ctx, int ggml_type, const void* table,
                          const unsigned int* ids, void* out_f16, int n, int hidden);
+
+/* ---------------------------------------------------------------------
+ * Decode-step support (f16 activations).  These are the non-GEMV launches
+ * of one batch-1 decode step of the reference's transformer family, each
+ * with the argument meaning of the CudaCtx method it replaces.  pos_dev,
+ * where accepted, is a device int holding the current position (graph
+ * replay); NULL uses the host value.  Attention needs head_dim 64 or 128,
+ * chunk sizes up to 512 and n_chunks * csz >= max_seq.
+ * --------------------------------------------------------------------- */
+
+/* y[r] = f16(sat(x[r]) * rsqrt(mean(sat(x[r])^2) + eps) * w) for rows
+ * r < rows of n elements; w NULL = unit weight.  CudaCtx::rmsnorm
+ * (src/cuda.rs:1180-1198). */
+int cima_hip_rmsnorm(cima_hip_ctx* ctx, const void* x, const void* w, void* y, int rows, int n, float eps);
+/* In-place NeoX RoPE over x [rows, heads, dim]; row r at position pos0 + r
+ * (or *pos_dev + r); pairs >= nfreqs unrotated.  CudaCtx::rope
+ * (src/cuda.rs:1302-1340) without frequency factors. */
+int cima_hip_rope(cima_hip_ctx* ctx, void* x, int rows, int heads, int dim, int pos0, float theta, int nfreqs,
+                  const int* pos_dev);
+/* k, v [rows, kv_heads*dim] -> caches [kv_heads, max_seq, dim] at position
+ * pos + r (or *pos_dev + r); positions >= max_seq are dropped.
+ * CudaCtx::kv_append (src/cuda.rs:1344-1375). */
+int cima_hip_kv_append(cima_hip_ctx* ctx, const void* k, const void* v, void* k_cache, void* v_cache, int rows,
+                       int kv_heads, int dim, int pos, int max_seq, const int* pos_dev);
+/* Per-(head, chunk) partial attention {m, l, acc[dim]} fp32 into part
+ * [q_heads, n_chunks, dim + 2] for the query q [q_heads, dim] against the
+ * first seq (or *pos_dev + 1) cache positions.  CudaCtx::attn_decode_split
+ * (src/cuda.rs:1418-1474). */
+int cima_hip_attn_decode_split(cima_hip_ctx* ctx, const void* q, const void* k_cache, const void* v_cache,
+                               float* part, int q_heads, int kv_heads, int dim, int seq, int max_seq, int csz,
+                               int n_chunks, float scale, int window, const int* pos_dev);
+/* Log-sum-exp merge of the partials into out [q_heads, dim] f16.
+ * CudaCtx::attn_reduce (src/cuda.rs:1476-1505). */
+int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_heads, int dim, int csz,
+                         int n_chunks, int seq, int max_seq, int window, const int* pos_dev);
+/* One launch for a layer's decode attention at position *pos_dev: RoPE of
+ * q and k from qkv = [q | k | v] (the fused q/k/v GEMV output), append of
+ * the new k and v to the caches, split attention and merge into out
+ * [q_heads, dim].  Replaces rope x2 + kv_append + attn_decode_split +
+ * attn_reduce (src/models/transformer.rs:1100-1173).  counters: q_heads
+ * unsigned ints, zero before the first call and left zero by every call;
+ * part as for the split kernel.  Calls that overlap on one device must not
+ * share counters or part. */
+int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* k_cache, void* v_cache, float* part,
+                         unsigned int* counters, void* out, int q_heads, int kv_heads, int dim, int max_seq, int csz,
+                         int n_chunks, float theta, float scale, const int* pos_dev);
+/* Greedy argmax of f16 logits x[n] (softcap cap > 0: cap * tanh(x / cap))
+ * into *slot as (orderable f32 bits << 32 | index), ties to the higher
+ * index.  *slot must be 0 on entry (cima_hip_argmax_to_ids leaves it 0).
+ * CudaCtx::argmax_softcap_enqueue (src/cuda.rs:2036-2056) without its
+ * memset, which would not be safe to capture. */
+int cima_hip_argmax(cima_hip_ctx* ctx, const void* x, unsigned long long* slot, int n, float cap);
+/* ids[0] = index in *slot (ids may be NULL), *slot = 0, and *pos_dev += 1
+ * when pos_dev is not NULL: CudaCtx::argmax_to_ids + pos_bump
+ * (src/cuda.rs:2058-2073). */
+int cima_hip_argmax_to_ids(cima_hip_ctx* ctx, unsigned long long* slot, unsigned int* ids, int* pos_dev);
+/* *pos_dev += 1: CudaCtx::pos_bump (src/cuda.rs:2068-2073). */
+int cima_hip_pos_bump(cima_hip_ctx* ctx, int* pos_dev);
+
+/* One layer of a Qwen2/Llama-family decoder, weights in GGUF blocks. */
+typedef struct cima_decoder_layer {
+    const void* attn_norm;  /* f16 [hidden] */
+    const void* wqkv;       /* [(q_heads + 2 kv_heads) * head_dim, hidden]: q rows, k rows, v rows */
+    const void* bqkv;       /* f16 [(q_heads + 2 kv_heads) * head_dim], or NULL */
+    const void* wo;         /* [hidden, q_heads * head_dim] */
+    const void* ffn_norm;   /* f16 [hidden] */
+    const void* w_gate_up;  /* [2 ffn, hidden]: gate rows then up rows */
+    const void* w_down;     /* [hidden, ffn] */
+    void* k_cache;          /* f16 [kv_heads, max_seq, head_dim] */
+    void* v_cache;          /* f16 [kv_heads, max_seq, head_dim] */
+} cima_decoder_layer;
+
+/* A decoder and its device workspace for cima_hip_decode_step. */
+typedef struct cima_decoder {
+    int ggml_type;    /* block format of every layer weight */
+    int embed_type;   /* block format of the embedding table */
+    int head_type;    /* block format of head (ignored when tied) */
+    int n_layers, hidden, q_heads, kv_heads, head_dim, ffn, vocab, max_seq;
+    int attn_chunk;   /* positions per attention chunk (0 = 128) */
+    float rope_theta, rms_eps;
+    const void* embed;       /* [vocab, hidden] */
+    const void* head;        /* [vocab, hidden], NULL = tied to embed */
+    const void* final_norm;  /* f16 [hidden] */
+    const cima_decoder_layer* layers;  /* host array of n_layers */
+    /* workspace, all device memory */
+    void* x;          /* f16 [hidden] residual stream */
+    void* qkv;        /* f16 [(q_heads + 2 kv_heads) * head_dim] */
+    void* att;        /* f16 [q_heads * head_dim] */
+    void* act;        /* f16 [ffn] */
+    void* logits;     /* f16 [vocab] */
+    float* part;      /* q_heads * ceil(max_seq / attn_chunk) * (head_dim + 2) floats */
+    unsigned int* counters;    /* q_heads, zero */
+    unsigned long long* slot;  /* zero */
+    unsigned int* ids;         /* [1]: input token; receives the greedy next token */
+    int* pos;                  /* [1]: position of the input token; advanced by one */
+} cima_decoder;
+
+/* One greedy batch-1 decode step, all on the context's stream and safe to
+ * capture in a HIP graph (positions come from *pos, nothing is allocated):
+ * gather ids[0] -> per layer [rmsnorm + q|k|v GEMV + bias, fused attention,
+ * o GEMV + residual, rmsnorm + gate|up SwiGLU GEMV, down GEMV + residual]
+ * -> rmsnorm + head GEMV -> argmax -> ids[0], pos += 1.  Replaces
+ * enqueue_decode_device (src/models/transformer.rs:1440-1461) and
+ * forward_chunk_at's rows == 1 path (:1012-1300): 5 launches per layer
+ * where the reference issues about 12. */
+int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d);
 
 #ifdef __cplusplus
 }

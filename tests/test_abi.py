@@ -58,6 +58,35 @@ def test_code_object_holds_every_kernel():
                     assert f"cima_gemm_{f}_b{bn}_{xt}_{yt}".encode() in blobs["gemm"]
 
 
+def test_decode_object_holds_every_kernel():
+    blob = open(cbuild.HSACOS["decode"], "rb").read()
+    names = ["cima_rmsnorm_f16", "cima_rope_f16", "cima_kv_append_f16", "cima_argmax_f16", "cima_argmax_to_ids",
+             "cima_pos_bump"]
+    names += [f"cima_attn_{k}_d{d}" for k in ("split", "reduce", "decode") for d in (64, 128)]
+    for n in names:
+        assert n.encode() in blob, n
+
+
+def test_decoder_struct_layout_matches_header(tmp_path):
+    """The ctypes mirrors of cima_decoder / cima_decoder_layer have the C
+    layout (compiled with the header by the host compiler)."""
+    src = tmp_path / "layout.c"
+    fields = [f[0] for f in hipmod.Decoder._fields_]
+    lfields = [f[0] for f in hipmod.DecoderLayer._fields_]
+    body = "".join(f'printf("%zu ", offsetof(cima_decoder, {f}));' for f in fields)
+    body += "".join(f'printf("%zu ", offsetof(cima_decoder_layer, {f}));' for f in lfields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "cima_hip.h"\nint main(void){'
+                   + body + 'printf("%zu %zu", sizeof(cima_decoder), sizeof(cima_decoder_layer));return 0;}')
+    exe = tmp_path / "layout"
+    import subprocess
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [getattr(hipmod.Decoder, f).offset for f in fields] + [getattr(hipmod.DecoderLayer, f).offset
+                                                                    for f in lfields]
+    want += [ctypes.sizeof(hipmod.Decoder), ctypes.sizeof(hipmod.DecoderLayer)]
+    assert got == want
+
+
 def test_error_classification():
     L = hipmod.load_library()
     for c in (700, 702, 710, 713, 719):

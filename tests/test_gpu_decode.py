@@ -1,0 +1,351 @@
+"""GPU parity of the decode-step kernels (cima_decode.hsaco) and of the
+fused RMSNorm -> GEMV against the CPU oracle (oracle/decode.py), and of a
+whole greedy decode step against the oracle's restatement of the
+reference's decode order.
+
+Tolerances: element ops on f16 data are held to one or two f16 ulps of the
+float64 oracle (|d| <= 2^-9 |v| + small absolute slack for RoPE's fp32
+angles); GEMVs to the north star's 1e-3 normwise relative error; a full
+step's logits to 1e-2 normwise (two dozen chained f16 roundings, each a
+possible ulp apart) with the greedy token equal unless the oracle's top two
+logits are within that tolerance."""
+import numpy as np
+import pytest
+
+import oracle
+from oracle import decode as od
+from cima_amd import gguf, synth
+from cima_amd.decoder import DecoderConfig, DeviceDecoder, synthetic_kv, synthetic_model
+from cima_amd.hip import E_INVALID, EngineError
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K = 8, 12
+
+
+def dev16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float16)).cuda()
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def ulps_ok(got, want, ulps=2, atol=0.0):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return np.all(np.abs(got - want) <= ulps * 2.0 ** -10 * np.abs(want) + atol + 2.0 ** -24)
+
+
+# ----------------------------------------------------------------- norms
+
+@pytest.mark.parametrize("rows,n", [(1, 896), (3, 4096), (2, 100)])
+def test_rmsnorm(hip, rows, n):
+    x = (4 * np.random.default_rng(n).normal(size=(rows, n))).astype(np.float16)
+    x[0, 0] = 65504.0  # saturates
+    w = (1 + 0.1 * np.random.default_rng(1).normal(size=n)).astype(np.float16)
+    y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+    hip.rmsnorm(dev16(x), dev16(w), y, rows, n, 1e-6)
+    assert ulps_ok(host(y), od.rmsnorm(x, w, 1e-6), ulps=1)
+    hip.rmsnorm(dev16(x), None, y, rows, n, 1e-6)
+    assert ulps_ok(host(y), od.rmsnorm(x, None, 1e-6), ulps=1)
+
+
+@pytest.mark.parametrize("t,n,k,mode", [(Q8_0, 1152, 896, 0), (Q8_0, 4864, 896, 2), (Q4_K, 4096, 4096, 0),
+                                        (Q8_0, 896, 896, 1)])
+def test_rmsnorm_gemv_f16(hip, t, n, k, mode):
+    """rmsnorm folded into the GEMV's x staging equals rmsnorm -> GEMV."""
+    w = synth.weights(t, 21, 0.02, 2 * n if mode == 2 else n, k)
+    x = (3 * synth.normal(22, 1.0, k)).astype(np.float16)
+    g = (1 + synth.normal(23, 0.1, k)).astype(np.float16)
+    b = synth.normal(24, 0.1, 2 * n if mode == 2 else n).astype(np.float16)
+    y0 = synth.normal(25, 1.0, n).astype(np.float16)
+    y = dev16(y0)
+    hip.rmsnorm_gguf_gemv(t, dev16(x), dev16(g), 1e-6, torch.from_numpy(w).cuda(), dev16(b), y, n, k, mode)
+    got = host(y).astype(np.float64)
+    h = od.rmsnorm(x, g, 1e-6)[0]
+    rows = 2 * n if mode == 2 else n
+    dot = oracle.gguf_gemv_packed(t, w, h.astype(np.float32), rows, k, threads=8).astype(np.float64)
+    dot += b.astype(np.float64)
+    if mode == 2:
+        gg, uu = dot[:n], dot[n:]
+        want = gg / (1 + np.exp(-gg)) * uu
+    elif mode == 1:
+        want = y0.astype(np.float64) + dot
+    else:
+        want = dot
+    r = rel(got, want)
+    print(f"rmsnorm+gemv t={t} {n}x{k} mode {mode}: rel {r:.2e}")
+    assert r <= 1e-3
+
+
+def test_rmsnorm_gemv_f32(hip):
+    t, n, k = Q8_0, 500, 896
+    w = synth.weights(t, 31, 0.02, n, k)
+    x = synth.normal(32, 2.0, k)
+    g = 1 + synth.normal(33, 0.1, k)
+    y = torch.empty(n, device="cuda")
+    hip.rmsnorm_gguf_gemv(t, torch.from_numpy(x).cuda(), torch.from_numpy(g).cuda(), 1e-5,
+                          torch.from_numpy(w).cuda(), None, y, n, k, 0)
+    xs = x.astype(np.float64)
+    h = xs / np.sqrt((xs * xs).mean() + 1e-5) * g
+    want = oracle.gguf_gemv_packed(t, w, h.astype(np.float32), n, k)
+    assert rel(host(y), want) <= 1e-3
+
+
+# ------------------------------------------------------------ RoPE / KV
+
+@pytest.mark.parametrize("heads,dim,pos", [(14, 64, 2048), (32, 128, 77), (2, 64, 0)])
+def test_rope(hip, heads, dim, pos):
+    rows = 3
+    x = np.random.default_rng(dim + pos).normal(size=(rows, heads, dim)).astype(np.float16)
+    t = dev16(x)
+    hip.rope(t, rows, heads, dim, pos, 1e6, dim // 2)
+    want = od.rope(x, pos, 1e6)
+    # the angle p * freq is fp32 on both sides; cos/sin of it differ in the
+    # last fp32 bits, which can move an f16 rounding by one ulp
+    assert ulps_ok(host(t).reshape(rows, heads, dim), want, ulps=2, atol=2e-4)
+
+
+def test_rope_device_position_and_nfreqs(hip):
+    x = np.random.default_rng(3).normal(size=(1, 4, 64)).astype(np.float16)
+    t = dev16(x)
+    pos = torch.tensor([1234], dtype=torch.int32, device="cuda")
+    hip.rope(t, 1, 4, 64, 0, 1e4, 20, pos_dev=pos)
+    assert ulps_ok(host(t).reshape(1, 4, 64), od.rope(x, 1234, 1e4, nfreqs=20), ulps=2, atol=2e-4)
+
+
+def test_kv_append(hip):
+    kvh, dim, max_seq = 2, 64, 40
+    k = np.random.default_rng(4).normal(size=(3, kvh * dim)).astype(np.float16)
+    v = np.random.default_rng(5).normal(size=(3, kvh * dim)).astype(np.float16)
+    kc = torch.zeros((kvh, max_seq, dim), dtype=torch.float16, device="cuda")
+    vc = torch.zeros_like(kc)
+    hip.kv_append(dev16(k), dev16(v), kc, vc, 3, kvh, dim, 38, max_seq)  # row 2 would be 40: dropped
+    wk = np.zeros((kvh, max_seq, dim), np.float16)
+    wv = np.zeros_like(wk)
+    od.kv_append(wk, wv, k.reshape(3, kvh, dim), v.reshape(3, kvh, dim), 38)
+    assert np.all(host(kc) == wk) and np.all(host(vc) == wv)
+
+
+# ------------------------------------------------------------- attention
+
+def _attn_case(dim, q_heads, kv_heads, max_seq, seed):
+    r = np.random.default_rng(seed)
+    kc = r.normal(size=(kv_heads, max_seq, dim)).astype(np.float16)
+    vc = r.normal(size=(kv_heads, max_seq, dim)).astype(np.float16)
+    q = (0.5 * r.normal(size=(q_heads, dim))).astype(np.float16)
+    return q, kc, vc
+
+
+@pytest.mark.parametrize("dim,qh,kvh,seq,csz,window", [
+    (64, 14, 2, 2049, 128, 0), (64, 14, 2, 1, 128, 0), (128, 32, 8, 777, 128, 0),
+    (64, 4, 4, 1000, 256, 0), (64, 14, 2, 2049, 128, 300)])
+def test_attn_split_and_reduce(hip, dim, qh, kvh, seq, csz, window):
+    max_seq = 4096
+    q, kc, vc = _attn_case(dim, qh, kvh, max_seq, seq + dim)
+    nch = max_seq // csz
+    part = torch.zeros(qh * nch * (dim + 2), device="cuda")
+    out = torch.empty((qh, dim), dtype=torch.float16, device="cuda")
+    scale = 1 / np.sqrt(dim)
+    hip.attn_decode_split(dev16(q), dev16(kc), dev16(vc), part, qh, kvh, dim, seq, max_seq, csz, nch, scale,
+                          window)
+    hip.attn_reduce(part, out, qh, dim, csz, nch, seq, max_seq, window)
+    want = od.attention(q, kc, vc, seq, scale, window)
+    got = host(out).astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 2e-3, np.max(np.abs(got - want))
+    # the partials themselves: m and l per chunk
+    P = host(part).reshape(qh, nch, dim + 2)
+    ref = od.attn_partials(q, kc, vc, seq, scale, csz, nch, window)
+    for h in (0, qh - 1):
+        for c in range(nch):
+            if ref[h][c] is None:
+                continue
+            m, l, acc = ref[h][c]
+            assert abs(P[h, c, 0] - m) <= 1e-4 * max(1, abs(m))
+            assert abs(P[h, c, 1] - l) <= 1e-4 * l
+            assert np.allclose(P[h, c, 2:], acc, rtol=1e-3, atol=1e-3 * l)
+
+
+@pytest.mark.parametrize("dim,qh,kvh,pos", [(64, 14, 2, 2048), (64, 14, 2, 0), (128, 32, 8, 300),
+                                            (64, 14, 2, 127), (64, 14, 2, 128)])
+def test_attn_decode_fused(hip, dim, qh, kvh, pos):
+    """rope q, k + append + split + merge in one launch == the separate ops."""
+    max_seq, csz = 4096, 128
+    nch = max_seq // csz
+    r = np.random.default_rng(pos + dim)
+    kc = np.zeros((kvh, max_seq, dim), np.float16)
+    vc = np.zeros_like(kc)
+    kc[:, :pos] = r.normal(size=(kvh, pos, dim))
+    vc[:, :pos] = r.normal(size=(kvh, pos, dim))
+    qkv = (0.5 * r.normal(size=(qh + 2 * kvh) * dim)).astype(np.float16)
+    dkc, dvc = dev16(kc), dev16(vc)
+    part = torch.zeros(qh * nch * (dim + 2), device="cuda")
+    counters = torch.zeros(qh, dtype=torch.int32, device="cuda")
+    out = torch.empty((qh, dim), dtype=torch.float16, device="cuda")
+    posd = torch.tensor([pos], dtype=torch.int32, device="cuda")
+    scale = 1 / np.sqrt(dim)
+    for rep in range(2):  # counters must come back to zero
+        dkc2, dvc2 = dkc.clone(), dvc.clone()
+        hip.attn_decode(dev16(qkv), dkc2, dvc2, part, counters, out, qh, kvh, dim, max_seq, csz, nch, 1e6, scale,
+                        posd)
+        q = od.rope(qkv[:qh * dim].reshape(1, qh, dim), pos, 1e6)[0]
+        k = od.rope(qkv[qh * dim:(qh + kvh) * dim].reshape(1, kvh, dim), pos, 1e6)
+        v = qkv[(qh + kvh) * dim:].reshape(1, kvh, dim)
+        wk, wv = kc.copy(), vc.copy()
+        od.kv_append(wk, wv, k, v, pos)
+        want = od.attention(q, wk, wv, pos + 1, scale)
+        got = host(out).astype(np.float64)
+        assert np.max(np.abs(got - want)) <= 3e-3, (rep, np.max(np.abs(got - want)))
+        gk = host(dkc2)
+        assert ulps_ok(gk[:, pos], wk[:, pos], ulps=2, atol=2e-4)
+        assert np.all(host(dvc2)[:, pos] == wv[:, pos])
+        assert np.all(gk[:, :pos] == kc[:, :pos]) and np.all(gk[:, pos + 1:] == 0)
+        assert np.all(host(counters) == 0)
+
+
+def test_attention_argument_errors(hip):
+    part = torch.zeros(64, device="cuda")
+    z = torch.zeros(64, dtype=torch.float16, device="cuda")
+    with pytest.raises(EngineError) as e:  # head_dim 96 is not built
+        hip.attn_decode_split(z, z, z, part, 1, 1, 96, 1, 64, 64, 1, 0.1)
+    assert e.value.code == E_INVALID
+    with pytest.raises(EngineError):  # chunks do not cover max_seq
+        hip.attn_decode_split(z, z, z, part, 1, 1, 64, 1, 1024, 128, 4, 0.1)
+    with pytest.raises(EngineError):  # q heads not a multiple of kv heads
+        hip.attn_decode_split(z, z, z, part, 3, 2, 64, 1, 128, 128, 1, 0.1)
+
+
+# ---------------------------------------------------------------- argmax
+
+@pytest.mark.parametrize("n", [151936, 1000, 1])
+def test_argmax_and_feedback(hip, n):
+    x = (3 * np.random.default_rng(n).normal(size=n)).astype(np.float16)
+    if n > 10:
+        x[[7, n - 3]] = np.float16(20.0)  # tie -> higher index
+    slot = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ids = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pos = torch.tensor([41], dtype=torch.int32, device="cuda")
+    hip.argmax(dev16(x), slot, n)
+    idx, packed = od.argmax_packed(x)
+    assert int(host(slot).view(np.uint64)[0]) == packed
+    hip.argmax_to_ids(slot, ids, pos)
+    assert int(host(ids)[0]) == idx and int(host(slot)[0]) == 0 and int(host(pos)[0]) == 42
+    hip.pos_bump(pos)
+    assert int(host(pos)[0]) == 43
+
+
+def test_argmax_softcap(hip):
+    x = (10 * np.random.default_rng(2).normal(size=5000)).astype(np.float16)
+    slot = torch.zeros(1, dtype=torch.int64, device="cuda")
+    hip.argmax(dev16(x), slot, 5000, 30.0)
+    got = int(host(slot).view(np.uint64)[0])
+    idx, packed = od.argmax_packed(x, 30.0)
+    assert got & 0xFFFFFFFF == idx
+    # tanh in fp32 may differ in the last bit of the value half
+    assert abs((got >> 32) - (packed >> 32)) <= 2
+
+
+# ------------------------------------------------------------ decode step
+
+SMALL = DecoderConfig(n_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                      max_seq=512)
+
+
+def _oracle_model(m, kvs):
+    c = m.cfg
+    return dict(cfg=dict(hidden=c.hidden, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, ffn=c.ffn,
+                         vocab=c.vocab, rope_theta=c.rope_theta, rms_eps=c.rms_eps, type=int(c.ggml_type),
+                         embed_type=int(c.ggml_type)),
+                embed=m.embed, head=m.head, final_norm=m.final_norm,
+                layers=[dict(L, k_cache=kv[0].copy(), v_cache=kv[1].copy()) for L, kv in zip(m.layers, kvs)])
+
+
+def _check_step(logits_gpu, tok_gpu, logits_ref, tok_ref, tol):
+    r = rel(logits_gpu, logits_ref)
+    top = np.sort(logits_ref.astype(np.float64))[-2:]
+    print(f"decode step: logits rel err {r:.2e}, token {tok_gpu} (oracle {tok_ref}), top-2 gap {top[1] - top[0]:.3g}")
+    assert r <= tol
+    if tok_gpu != tok_ref:
+        assert top[1] - top[0] <= tol * np.abs(logits_ref.astype(np.float64)).max()
+
+
+def test_decode_steps_small_against_oracle(hip):
+    m = synthetic_model(SMALL, seed=3)
+    ctx_len = 300
+    kvs = [synthetic_kv(SMALL, i, ctx_len) for i in range(SMALL.n_layers)]
+    d = DeviceDecoder(hip, m)
+    for i, (kc, vc) in enumerate(kvs):
+        d.load_kv(i, kc, vc)
+    om = _oracle_model(m, kvs)
+    tok, pos = 17, ctx_len
+    d.set_state(tok, pos)
+    for s in range(3):
+        d.step()
+        torch.cuda.synchronize()
+        lg = host(d.logits)
+        ref_logits, ref_tok = od.decode_step(om, tok, pos)
+        _check_step(lg, d.token(), ref_logits, ref_tok, 1e-2)
+        assert d.position() == pos + 1
+        # continue both from the GPU's token so the trajectories stay aligned
+        tok, pos = d.token(), pos + 1
+        for i, L in enumerate(d.layers):  # the new k/v rows match the oracle's
+            assert np.max(np.abs(host(L["v_cache"])[:, pos - 1].astype(np.float64)
+                                 - om["layers"][i]["v_cache"][:, pos - 1])) <= 1e-2
+
+
+def test_decode_graph_replay_matches_eager(hip):
+    m = synthetic_model(SMALL, seed=4)
+    kvs = [synthetic_kv(SMALL, i, 100) for i in range(SMALL.n_layers)]
+    eager = DeviceDecoder(hip, m)
+    graph = DeviceDecoder(hip, m)
+    for d in (eager, graph):
+        for i, (kc, vc) in enumerate(kvs):
+            d.load_kv(i, kc, vc)
+        d.set_state(5, 100)
+    graph.capture()
+    for s in range(4):
+        eager.step()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.all(host(eager.logits) == host(graph.logits)), s
+        assert eager.token() == graph.token() and graph.position() == 101 + s
+        assert np.all(host(graph.counters) == 0)
+
+
+def test_decode_step_config5_full_size(hip):
+    """BASELINE config 5 (Qwen2.5-0.5B shape, Q8_0, KV prefilled to 2048):
+    one step against the oracle at full size."""
+    cfg = DecoderConfig()
+    m = synthetic_model(cfg, seed=5)
+    kvs = [synthetic_kv(cfg, i, 2048) for i in range(cfg.n_layers)]
+    d = DeviceDecoder(hip, m)
+    for i, (kc, vc) in enumerate(kvs):
+        d.load_kv(i, kc, vc)
+    d.set_state(1234, 2048)
+    d.capture()
+    d.replay()
+    torch.cuda.synchronize()
+    ref_logits, ref_tok = od.decode_step(_oracle_model(m, kvs), 1234, 2048, threads=16)
+    _check_step(host(d.logits), d.token(), ref_logits, ref_tok, 1e-2)
+    assert d.position() == 2049
+
+
+def test_decode_step_rejects_bad_descriptors(hip):
+    d = DeviceDecoder(hip, synthetic_model(DecoderConfig(n_layers=1, hidden=256, q_heads=4, kv_heads=2,
+                                                         head_dim=64, ffn=512, vocab=100, max_seq=256)))
+    d.desc.head_dim = 96
+    with pytest.raises(EngineError):
+        hip.decode_step(d.desc)
+    d.desc.head_dim = 64
+    d.desc.x = None
+    with pytest.raises(EngineError):
+        hip.decode_step(d.desc)
