@@ -232,24 +232,33 @@ def main():
             dd.load_kv(i, *synthetic_kv(dcfg, i, ctx_len))
         wbytes_tok = dm.embed.nbytes + sum(sum(v.nbytes for v in L.values() if v is not None) for L in dm.layers)
         del dm
+        def time_tokens(run, stream, n):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(n):
+                run()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / n
+
+        # per-launch (no graph) for reference, then the captured step
+        dd.set_state(1, ctx_len)
+        for _ in range(10):
+            dd.step()
+        eager_ms = time_tokens(dd.step, torch.cuda.current_stream(), 50)
         dd.set_state(1, ctx_len)
         dd.capture()
         for _ in range(20):
             dd.replay()
         torch.cuda.synchronize()
         p0 = dd.position()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(args.decode_tokens):
-            dd.replay()
-        b.record()
-        torch.cuda.synchronize()
-        dms = a.elapsed_time(b) / args.decode_tokens
+        dms = time_tokens(dd.replay, dd.stream, args.decode_tokens)
         assert dd.position() == p0 + args.decode_tokens
         kv_bytes = dcfg.n_layers * 2 * dcfg.kv_heads * dcfg.head_dim * 2 * (p0 + args.decode_tokens // 2)
         decode = {"workload": "qwen2.5-0.5b-shaped Q8_0 greedy decode step (24 layers, tied 151936 head), "
-                              "KV prefilled to 2048, one hipGraph replay per token (5 launches/layer + 4)",
+                              "KV prefilled to 2048, one hipGraph replay per token (5 launches/layer + 3)",
                   "tok_s": round(1e3 / dms, 1), "ms_per_token": round(dms, 4), "tokens": args.decode_tokens,
+                  "tok_s_without_graph": round(1e3 / eager_ms, 1),
                   "context": [p0, p0 + args.decode_tokens],
                   "bytes_per_token": wbytes_tok + kv_bytes,
                   "gb_s": round((wbytes_tok + kv_bytes) / dms / 1e6, 1)}

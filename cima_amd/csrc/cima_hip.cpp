@@ -142,6 +142,21 @@ void unload(cima_hip_ctx* ctx) {
     ctx->loaded = false;
 }
 
+// kernel-argument mirror of GemvExt in gguf_gemv.hip (same member order)
+struct GemvExt {
+    const void* norm_w;
+    float eps;
+    int att_chunks;
+    int att_csz;
+    int att_dim;
+    int max_seq;
+    const int* pos_dev;
+    unsigned long long* slot;
+};
+
+// extra x source / epilogue of a decode-step GEMV
+enum GemvKind { GK_PLAIN = 0, GK_ATT = 1, GK_AMAX = 2 };
+
 struct GemvPlan {
     int rows;        // R: rows per lane group
     int iters;       // unit steps per row and lane
@@ -187,7 +202,8 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
                 const void* ba, const void* bb, void* y, int n, int k, int mode, int act, bool pair,
-                const char* api, const void* norm_w = nullptr, float eps = 0.f) {
+                const char* api, const void* norm_w = nullptr, float eps = 0.f, GemvKind kind = GK_PLAIN,
+                const GemvExt* kext = nullptr) {
     if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
@@ -214,9 +230,21 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (p.iters > 8)
         return fail(CIMA_E_INVALID, "%s: k=%d is longer than the GEMV supports (%d units per lane group)", api, k,
                     p.iters);
-    const bool epi = ba != nullptr || bb != nullptr || mode == 1;
+    bool epi = ba != nullptr || bb != nullptr || mode == 1;
+    const char* kind_sfx = pair ? "_pair" : "";
+    if (kind == GK_ATT) {
+        kind_sfx = "_att";
+        epi = true;  // built with the epilogue only
+        p.lds = (unsigned)(((p.lds + 15u) & ~15u) + 4u * (unsigned)k);
+        if ((long)p.lds > ctx->max_lds)
+            return fail(CIMA_E_INVALID, "%s: k=%d needs %u B of LDS, the device allows %d", api, k, p.lds,
+                        ctx->max_lds);
+    } else if (kind == GK_AMAX) {
+        kind_sfx = "_amax";
+        if (epi) return fail(CIMA_E_INVALID, "%s: the argmax GEMV takes no bias or residual", api);
+    }
     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s", F->name, p.rows, p.iters,
-             act == CIMA_DT_F32 ? "f32" : "f16", pair ? "_pair" : "", epi ? "_epi" : "");
+             act == CIMA_DT_F32 ? "f32" : "f16", kind_sfx, epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
     int resident = 0;
@@ -234,10 +262,11 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     const void* b0 = ba;
     const void* b1 = bb;
     void* yy = y;
-    const void* nw = norm_w;
-    float ep = eps;
+    GemvExt ext = kext ? *kext : GemvExt{};
+    ext.norm_w = norm_w;
+    ext.eps = eps;
     int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
-    void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls, &nw, &ep};
+    void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls, &ext};
     return launch(ctx, f, p.grid, 256, args, api, p.lds);
 }
 
@@ -288,7 +317,9 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         const Fmt* F = fmt_of(t);
         for (const auto& sh : kShapes)
             for (const char* act : {"f32", "f16"})
-                for (const char* sfx : {"", "_epi", "_pair", "_pair_epi"}) {
+                for (const char* sfx : {"", "_epi", "_pair", "_pair_epi", "_att_epi", "_amax"}) {
+                    if (!strcmp(act, "f32") && (!strcmp(sfx, "_att_epi") || !strcmp(sfx, "_amax")))
+                        continue;  // attention / argmax variants are f16 only
                     char name[96];
                     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
                     if (!rc) rc = add(0, name);
@@ -550,23 +581,25 @@ int launch_named(cima_hip_ctx* ctx, const char* name, unsigned grid, unsigned bl
 
 int attn_dim_ok(int dim) { return dim == 64 || dim == 128; }
 
-int attn_fused(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, unsigned* counters, void* out,
-               int q_heads, int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
-               const int* pos_dev, const char* api) {
+// positions per attention chunk the kernels stage at most (ATT_MAX_CSZ)
+const int kAttMaxChunk = 256;
+
+int attn_fused(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, int q_heads, int kv_heads,
+               int dim, int max_seq, int csz, int n_chunks, float theta, float scale, const int* pos_dev,
+               const char* api) {
     if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || !attn_dim_ok(dim) || max_seq <= 0 || csz <= 0 ||
-        csz > 512 || n_chunks <= 0 || (long long)n_chunks * csz < max_seq)
+        csz > kAttMaxChunk || n_chunks <= 0 || (long long)n_chunks * csz < max_seq)
         return fail(CIMA_E_INVALID,
                     "%s: q_heads=%d kv_heads=%d dim=%d max_seq=%d csz=%d n_chunks=%d (dim 64 or 128, q_heads a "
-                    "multiple of kv_heads, csz <= 512, n_chunks * csz >= max_seq)",
+                    "multiple of kv_heads, csz <= 256, n_chunks * csz >= max_seq)",
                     api, q_heads, kv_heads, dim, max_seq, csz, n_chunks);
-    if (!qkv || !kc || !vc || !part || !counters || !out || !pos_dev)
-        return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    if (!qkv || !kc || !vc || !part || !pos_dev) return fail(CIMA_E_INVALID, "%s: null pointer", api);
     if (!aligned(kc, 16) || !aligned(vc, 16) || !aligned(qkv, 4))
         return fail(CIMA_E_INVALID, "%s: misaligned cache (16 B) or qkv (4 B)", api);
     char name[48];
     snprintf(name, sizeof name, "cima_attn_decode_d%d", dim);
-    void* args[] = {&qkv, &kc, &vc, &part, &counters, &out, &q_heads, &kv_heads, &max_seq, &csz, &n_chunks,
-                    &theta, &scale, &pos_dev};
+    void* args[] = {&qkv, &kc, &vc, &part, &q_heads, &kv_heads, &max_seq, &csz, &n_chunks, &theta, &scale,
+                    &pos_dev};
     return launch_named(ctx, name, (unsigned)(q_heads * n_chunks), 256, args, api);
 }
 
@@ -611,7 +644,7 @@ int cima_hip_attn_decode_split(cima_hip_ctx* ctx, const void* q, const void* kc,
     const char* api = "cima_hip_attn_decode_split";
     if (int rc = ready(ctx, api)) return rc;
     if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || !attn_dim_ok(dim) || max_seq <= 0 || csz <= 0 ||
-        csz > 512 || n_chunks <= 0 || (long long)n_chunks * csz < max_seq || seq < 0 || window < 0)
+        csz > kAttMaxChunk || n_chunks <= 0 || (long long)n_chunks * csz < max_seq || seq < 0 || window < 0)
         return fail(CIMA_E_INVALID, "%s: q_heads=%d kv_heads=%d dim=%d seq=%d max_seq=%d csz=%d n_chunks=%d", api,
                     q_heads, kv_heads, dim, seq, max_seq, csz, n_chunks);
     if (!q || !kc || !vc || !part) return fail(CIMA_E_INVALID, "%s: null pointer", api);
@@ -636,13 +669,43 @@ int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_
     return launch_named(ctx, name, (unsigned)q_heads, 256, args, api);
 }
 
-int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, unsigned* counters,
-                         void* out, int q_heads, int kv_heads, int dim, int max_seq, int csz, int n_chunks,
-                         float theta, float scale, const int* pos_dev) {
+int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, int q_heads,
+                         int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
+                         const int* pos_dev) {
     const char* api = "cima_hip_attn_decode";
     if (int rc = ready(ctx, api)) return rc;
-    return attn_fused(ctx, qkv, kc, vc, part, counters, out, q_heads, kv_heads, dim, max_seq, csz, n_chunks, theta,
-                      scale, pos_dev, api);
+    return attn_fused(ctx, qkv, kc, vc, part, q_heads, kv_heads, dim, max_seq, csz, n_chunks, theta, scale, pos_dev,
+                      api);
+}
+
+int cima_hip_attn_gguf_gemv(cima_hip_ctx* ctx, int t, const float* part, int q_heads, int dim, int csz, int n_chunks,
+                            int max_seq, const int* pos_dev, const void* w, const void* bias, void* y, int n, int mode) {
+    const char* api = "cima_hip_attn_gguf_gemv";
+    if (int rc = ready(ctx, api)) return rc;
+    if (q_heads <= 0 || !attn_dim_ok(dim) || csz <= 0 || n_chunks <= 0 || max_seq <= 0 || (mode != 0 && mode != 1))
+        return fail(CIMA_E_INVALID, "%s: q_heads=%d dim=%d csz=%d n_chunks=%d max_seq=%d mode=%d", api, q_heads, dim,
+                    csz, n_chunks, max_seq, mode);
+    if (!part || !pos_dev) return fail(CIMA_E_INVALID, "%s: null partials or position", api);
+    if (!aligned(part, 8)) return fail(CIMA_E_INVALID, "%s: partials must be 8-byte aligned", api);
+    GemvExt ext{};
+    ext.att_chunks = n_chunks;
+    ext.att_csz = csz;
+    ext.att_dim = dim;
+    ext.max_seq = max_seq;
+    ext.pos_dev = pos_dev;
+    return gemv_common(ctx, t, part, w, nullptr, bias, nullptr, y, n, q_heads * dim, mode, CIMA_DT_F16, false, api,
+                       nullptr, 0.f, GK_ATT, &ext);
+}
+
+int cima_hip_gguf_gemv_argmax(cima_hip_ctx* ctx, int t, const void* x, const void* norm_w, float eps, const void* w,
+                              void* y, int n, int k, unsigned long long* slot) {
+    const char* api = "cima_hip_gguf_gemv_argmax";
+    if (int rc = ready(ctx, api)) return rc;
+    if (!slot || !aligned(slot, 8)) return fail(CIMA_E_INVALID, "%s: null or misaligned slot", api);
+    GemvExt ext{};
+    ext.slot = slot;
+    return gemv_common(ctx, t, x, w, nullptr, nullptr, nullptr, y, n, k, 0, CIMA_DT_F16, false, api, norm_w, eps,
+                       GK_AMAX, &ext);
 }
 
 int cima_hip_argmax(cima_hip_ctx* ctx, const void* x, unsigned long long* slot, int n, float cap) {
@@ -679,10 +742,11 @@ int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
     if (d->n_layers <= 0 || d->hidden <= 0 || d->ffn <= 0 || d->vocab <= 0 || d->q_heads <= 0 || d->kv_heads <= 0)
         return fail(CIMA_E_INVALID, "%s: layers=%d hidden=%d ffn=%d vocab=%d heads=%d/%d", api, d->n_layers,
                     d->hidden, d->ffn, d->vocab, d->q_heads, d->kv_heads);
-    if (!d->x || !d->qkv || !d->att || !d->act || !d->logits || !d->part || !d->counters || !d->slot || !d->ids ||
-        !d->pos || !d->embed || !d->final_norm)
+    if (!d->x || !d->qkv || !d->act || !d->logits || !d->part || !d->slot || !d->ids || !d->pos || !d->embed ||
+        !d->final_norm)
         return fail(CIMA_E_INVALID, "%s: null workspace, embedding or final norm pointer", api);
-    const int csz = d->attn_chunk > 0 ? d->attn_chunk : 128;
+    const int csz = d->attn_chunk > 0 ? d->attn_chunk : kAttMaxChunk;
+    if (csz > kAttMaxChunk) return fail(CIMA_E_INVALID, "%s: attn_chunk %d > %d", api, csz, kAttMaxChunk);
     const int nch = (d->max_seq + csz - 1) / csz;
     const float scale = 1.0f / sqrtf((float)hd);
     const void* head = d->head ? d->head : d->embed;
@@ -695,12 +759,13 @@ int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
         if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.attn_norm, d->rms_eps, L.wqkv, L.bqkv,
                                                 d->qkv, qd + 2 * kvd, d->hidden, 0, CIMA_DT_F16))
             return rc;
-        // rope q, k; kv append; split attention + merge (:1100-1173)
-        if (int rc = attn_fused(ctx, d->qkv, L.k_cache, L.v_cache, d->part, d->counters, d->att, d->q_heads,
-                                d->kv_heads, hd, d->max_seq, csz, nch, d->rope_theta, scale, d->pos, api))
+        // rope q, k; kv append; split attention (:1100-1160)
+        if (int rc = attn_fused(ctx, d->qkv, L.k_cache, L.v_cache, d->part, d->q_heads, d->kv_heads, hd, d->max_seq,
+                                csz, nch, d->rope_theta, scale, d->pos, api))
             return rc;
-        // o projection + residual (:1238)
-        if (int rc = cima_hip_gguf_gemv(ctx, d->ggml_type, d->att, L.wo, nullptr, d->x, d->hidden, qd, 1, CIMA_DT_F16))
+        // merge of the partials -> o projection + residual (:1161-1238)
+        if (int rc = cima_hip_attn_gguf_gemv(ctx, d->ggml_type, d->part, d->q_heads, hd, csz, nch, d->max_seq, d->pos,
+                                             L.wo, nullptr, d->x, d->hidden, 1))
             return rc;
         // rmsnorm -> gate|up SwiGLU -> down + residual (:1240-1260)
         if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.ffn_norm, d->rms_eps, L.w_gate_up,
@@ -710,12 +775,54 @@ int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
                                         CIMA_DT_F16))
             return rc;
     }
-    // final norm -> head -> argmax -> ids[0], pos += 1
-    if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, head_type, d->x, d->final_norm, d->rms_eps, head, nullptr,
-                                            d->logits, d->vocab, d->hidden, 0, CIMA_DT_F16))
+    // final norm -> head with argmax -> ids[0], pos += 1
+    if (int rc = cima_hip_gguf_gemv_argmax(ctx, head_type, d->x, d->final_norm, d->rms_eps, head, d->logits, d->vocab,
+                                           d->hidden, d->slot))
         return rc;
-    if (int rc = cima_hip_argmax(ctx, d->logits, d->slot, d->vocab, 0.f)) return rc;
     return cima_hip_argmax_to_ids(ctx, d->slot, d->ids, d->pos);
+}
+
+// ---------------------------------------------------------------- graphs
+
+struct cima_hip_graph {
+    hipGraphExec_t exec = nullptr;
+};
+
+int cima_hip_capture_begin(cima_hip_ctx* ctx) {
+    if (int rc = ready(ctx, "cima_hip_capture_begin")) return rc;
+    hipError_t e = hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeGlobal);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipStreamBeginCapture");
+}
+
+int cima_hip_capture_end(cima_hip_ctx* ctx, cima_hip_graph** out) {
+    if (int rc = ready(ctx, "cima_hip_capture_end")) return rc;
+    if (!out) return fail(CIMA_E_INVALID, "cima_hip_capture_end: null out pointer");
+    *out = nullptr;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &graph);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiateWithFlags(&exec, graph, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiateWithFlags");
+    auto* g = new cima_hip_graph();
+    g->exec = exec;
+    *out = g;
+    return 0;
+}
+
+int cima_hip_graph_launch(cima_hip_ctx* ctx, cima_hip_graph* g) {
+    if (int rc = ready(ctx, "cima_hip_graph_launch")) return rc;
+    if (!g || !g->exec) return fail(CIMA_E_INVALID, "cima_hip_graph_launch: null graph");
+    hipError_t e = hipGraphLaunch(g->exec, ctx->stream);
+    return e == hipSuccess ? 0 : hip_fail(e, "hipGraphLaunch");
+}
+
+int cima_hip_graph_destroy(cima_hip_graph* g) {
+    if (!g) return 0;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    delete g;
+    return 0;
 }
 
 }  // extern "C"

@@ -8,8 +8,8 @@
 // Every kernel reads and writes f16 activations (the engine's activation
 // type) and computes in fp32.  The standalone kernels keep the reference's
 // argument meaning (src/kernels.cu:37-50, 244-262, 397-454, 547-639) so they
-// are drop-ins one by one; cima_attn_decode_* fuses RoPE, the KV append, the
-// per-chunk attention and the merge of one layer into a single launch.
+// are drop-ins one by one; cima_attn_decode_* fuses RoPE, the KV append and
+// the per-chunk attention of one layer into a single launch.
 #include "gguf_formats.h"
 
 // |v| clamped to 65000 (g_sat16, src/kernels.cu:30-35)
@@ -113,65 +113,88 @@ extern "C" __global__ __launch_bounds__(256) void cima_kv_append_f16(const uint1
 // the chunk's maximum score, l = sum exp(score - m), acc = sum exp(score -
 // m) * v -- the reference's layout (src/kernels.cu:547-610), so the split
 // and merge kernels below interoperate with it.
+//
+// A workgroup of 256 threads takes one chunk of at most 256 positions of
+// one query head.  Every load of the chunk is issued before any of them is
+// used -- thread t's key row (position s0 + t) and a 1/256 slice of the
+// chunk's value rows -- so a chunk costs one memory round trip even when
+// the cache is cold in HBM; the values go through LDS to the weighted sum.
 
-constexpr int ATT_MAX_CSZ = 512;
+constexpr int ATT_MAX_CSZ = 256;
 
 template <int D>
 struct AttnLds {
+    uint16_t v[ATT_MAX_CSZ * D];  // the chunk's value rows (f16)
     float q[D];
     float kn[D];
     float vn[D];
     float p[ATT_MAX_CSZ];
     float red[8];
     float acc[512 / D][D];  // one accumulator row per position group
-    int last;
 };
 
-// One chunk [s0, s1) of one query head against the cache rows kh / vh
-// ([max_seq, D] f16).  Position `snew` (if in the chunk) takes its key and
-// value from L.kn / L.vn.  256 threads: scores one position per thread,
-// then lane pairs of dims x position groups for the weighted value sum.
-// Writes {m, l, acc} to `dst`.
+// The chunk's loads, held in registers until used: thread t's key row
+// (position s0 + t, clamped into the chunk) and value slice t + 256 j of the
+// chunk's contiguous value rows (clamped likewise).
 template <int D>
-DEV void attn_chunk(AttnLds<D>& L, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh, int s0,
-                    int s1, int snew, float scale, float* __restrict__ dst) {
+struct AttnRegs {
+    uint4 k[D / 8];
+    uint4 v[D / 8];
+};
+
+template <int D>
+DEV void attn_issue(AttnRegs<D>& R, const uint16_t* __restrict__ kh, const uint16_t* __restrict__ vh, int s0,
+                    int s1) {
+    constexpr int RV = D / 8;
     const int t = threadIdx.x, len = s1 - s0;
-    float mloc = -INFINITY;
-    for (int j = t; j < len; j += 256) {
-        const int s = s0 + j;
-        float d = 0.f;
-        if (s == snew) {
+    const uint4* kp = reinterpret_cast<const uint4*>(kh + (size_t)(s0 + min(t, len - 1)) * D);
 #pragma unroll
-            for (int e = 0; e < D; e++) d += L.q[e] * L.kn[e];
-        } else {
-            const uint4* kr = reinterpret_cast<const uint4*>(kh + (size_t)s * D);
+    for (int c = 0; c < RV; c++) R.k[c] = kp[c];
+    const uint4* vp = reinterpret_cast<const uint4*>(vh + (size_t)s0 * D);
 #pragma unroll
-            for (int c = 0; c < D / 8; c++) {
-                const uint4 u = kr[c];
-                const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    for (int j = 0; j < RV; j++) R.v[j] = vp[min(t + 256 * j, len * RV - 1)];
+}
+
+// Chunk [s0, s1) of one query head (q in L.q, fp32) from the loads in R;
+// position `snew` (if in the chunk) takes its key and value from L.kn /
+// L.vn.  Writes {m, l, acc} to dst.
+template <int D>
+DEV void attn_chunk(AttnLds<D>& L, const AttnRegs<D>& R, int s0, int s1, int snew, float scale,
+                    float* __restrict__ dst) {
+    constexpr int RV = D / 8;
+    const int t = threadIdx.x, len = s1 - s0;
+    // values -> LDS (slots past the chunk take clamped copies, never read)
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    d += L.q[8 * c + 2 * e] * h2f(w[e] & 0xffffu);
-                    d += L.q[8 * c + 2 * e + 1] * h2f(w[e] >> 16);
-                }
+    for (int j = 0; j < RV; j++) reinterpret_cast<uint4*>(L.v)[t + 256 * j] = R.v[j];
+    // score of position s0 + t
+    float d = 0.f;
+    if (s0 + t == snew) {
+#pragma unroll
+        for (int e = 0; e < D; e++) d += L.q[e] * L.kn[e];
+    } else {
+#pragma unroll
+        for (int c = 0; c < RV; c++) {
+            const uint32_t w[4] = {R.k[c].x, R.k[c].y, R.k[c].z, R.k[c].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                d += L.q[8 * c + 2 * e] * h2f(w[e] & 0xffffu);
+                d += L.q[8 * c + 2 * e + 1] * h2f(w[e] >> 16);
             }
         }
-        const float sc = d * scale;
-        L.p[j] = sc;
-        mloc = fmaxf(mloc, sc);
     }
-    mloc = wave_max(mloc);
-    if ((t & 63) == 0) L.red[t >> 6] = mloc;
+    const bool live = t < len;
+    const float sc = live ? d * scale : -INFINITY;
+    const float mw = wave_max(sc);
+    if ((t & 63) == 0) L.red[t >> 6] = mw;
     __syncthreads();
+    // the new position's value row replaces what the cache held there
+    const int rnew = snew - s0;
+    if (rnew >= 0 && rnew < len && t < D) L.v[rnew * D + t] = (uint16_t)f2h(L.vn[t]);
     const float M = fmaxf(fmaxf(L.red[0], L.red[1]), fmaxf(L.red[2], L.red[3]));
-    float lsum = 0.f;
-    for (int j = t; j < len; j += 256) {
-        const float e = __expf(L.p[j] - M);
-        L.p[j] = e;
-        lsum += e;
-    }
-    lsum = wave_sum(lsum);
-    if ((t & 63) == 0) L.red[4 + (t >> 6)] = lsum;
+    const float e = live ? __expf(sc - M) : 0.f;
+    L.p[t] = e;
+    const float lw = wave_sum(e);
+    if ((t & 63) == 0) L.red[4 + (t >> 6)] = lw;
     __syncthreads();
     // weighted value sum: lane pair dp owns dims 2dp, 2dp+1; G groups
     // stride the positions
@@ -179,19 +202,10 @@ DEV void attn_chunk(AttnLds<D>& L, const uint16_t* __restrict__ kh, const uint16
     const int dp = t % (D / 2), g = t / (D / 2);
     float a0 = 0.f, a1 = 0.f;
     for (int j = g; j < len; j += G) {
-        const int s = s0 + j;
         const float pj = L.p[j];
-        float v0, v1;
-        if (s == snew) {
-            v0 = L.vn[2 * dp];
-            v1 = L.vn[2 * dp + 1];
-        } else {
-            const uint32_t u = reinterpret_cast<const uint32_t*>(vh + (size_t)s * D)[dp];
-            v0 = h2f(u & 0xffffu);
-            v1 = h2f(u >> 16);
-        }
-        a0 += pj * v0;
-        a1 += pj * v1;
+        const uint32_t u = reinterpret_cast<const uint32_t*>(L.v + j * D)[dp];
+        a0 += pj * h2f(u & 0xffffu);
+        a1 += pj * h2f(u >> 16);
     }
     L.acc[g][2 * dp] = a0;
     L.acc[g][2 * dp + 1] = a1;
@@ -209,20 +223,23 @@ DEV void attn_chunk(AttnLds<D>& L, const uint16_t* __restrict__ kh, const uint16
 }
 
 // Merge chunks [c0, active) of one head: out = sum_c e^(m_c - M) acc_c /
-// sum_c e^(m_c - M) l_c (k_attn_reduce, src/kernels.cu:614-639).  Threads
-// t < D each produce one output element.
+// sum_c e^(m_c - M) l_c (k_attn_reduce, src/kernels.cu:614-639), with a
+// running maximum so every chunk is read once.  Threads t < D each produce
+// one output element.
 template <int D>
 DEV void attn_merge(const float* __restrict__ ph, int c0, int active, uint16_t* __restrict__ oh) {
     const int t = threadIdx.x;
     if (t >= D) return;
-    float M = -INFINITY;
-    for (int c = c0; c < active; c++) M = fmaxf(M, ph[(size_t)c * (D + 2)]);
-    float Ls = 0.f, a = 0.f;
+    float M = -INFINITY, Ls = 0.f, a = 0.f;
+#pragma unroll 4
     for (int c = c0; c < active; c++) {
         const float* pc = ph + (size_t)c * (D + 2);
-        const float w = __expf(pc[0] - M);
-        Ls += w * pc[1];
-        a += w * pc[2 + t];
+        const float m = pc[0], l = pc[1], v = pc[2 + t];
+        const float Mn = fmaxf(M, m);
+        const float so = __expf(M - Mn), sn = __expf(m - Mn);
+        Ls = Ls * so + l * sn;
+        a = a * so + v * sn;
+        M = Mn;
     }
     oh[t] = (uint16_t)f2h(a / Ls);
 }
@@ -237,8 +254,8 @@ DEV void attn_range(int& seq, int max_seq, int window, const int* pos_dev, int& 
 }
 
 // Split decode attention (k_attn_decode_split, src/kernels.cu:547-610): one
-// workgroup per (query head, chunk of csz positions); q [q_heads, D] f16
-// already rotated; GQA maps head h to kv head h / (q_heads / kv_heads).
+// workgroup per (query head, chunk of csz <= 256 positions); q [q_heads, D]
+// f16 already rotated; GQA maps head h to kv head h / (q_heads / kv_heads).
 // Chunks past the live length write nothing.
 template <int D>
 DEV void attn_split_body(const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -252,10 +269,11 @@ DEV void attn_split_body(const uint16_t* __restrict__ q, const uint16_t* __restr
     const int s0 = max(ci * csz, wlo), s1 = min(ci * csz + csz, seq);
     if (s0 >= s1) return;
     const int kvh = h / (q_heads / kv_heads);
+    AttnRegs<D> R;
+    attn_issue<D>(R, kc + (size_t)kvh * max_seq * D, vc + (size_t)kvh * max_seq * D, s0, s1);
     if (threadIdx.x < D) L.q[threadIdx.x] = h2f(q[(size_t)h * D + threadIdx.x]);
     __syncthreads();
-    attn_chunk<D>(L, kc + (size_t)kvh * max_seq * D, vc + (size_t)kvh * max_seq * D, s0, s1, -1, scale,
-                  part + ((size_t)h * n_chunks + ci) * (D + 2));
+    attn_chunk<D>(L, R, s0, s1, -1, scale, part + ((size_t)h * n_chunks + ci) * (D + 2));
 }
 
 template <int D>
@@ -268,23 +286,21 @@ DEV void attn_reduce_body(const float* __restrict__ part, uint16_t* __restrict__
     attn_merge<D>(part + (size_t)h * n_chunks * (D + 2), wlo / csz, active, out + (size_t)h * D);
 }
 
-// Fused decode attention of one layer at position pos = *pos_dev:
+// Decode attention partials of one layer at position pos = *pos_dev, with
+// RoPE and the KV append folded in:
 //   qkv = [q (q_heads*D) | k (kv_heads*D) | v (kv_heads*D)] f16, the output
 //   of the fused q/k/v GEMV (biases applied, RoPE not yet);
 //   every workgroup (query head h, chunk ci) rotates its q; the chunk that
-//   holds pos also rotates the new k, takes the new k and v from registers
-//   for position pos, and (first head of each kv group) appends them to the
-//   cache; the chunk's partial goes to `part`; the last workgroup of head h
-//   to finish (an agent-scope counter per head, counters[h], left at 0 for
-//   the next launch) merges the head's partials into out [q_heads, D].
-// Replaces k_rope x2 + k_kv_append + k_attn_decode_split + k_attn_reduce
-// (src/models/transformer.rs:1100-1173).  counters must hold zeros before
-// the first launch; `part` holds q_heads * n_chunks * (D + 2) floats.
+//   holds pos also rotates the new k, takes the new k and v from LDS for
+//   position pos, and (first head of each kv group) appends them to the
+//   cache.  The partials are merged by the consumer: attn_reduce, or the
+//   o-projection GEMV's x staging (cima_hip_attn_gguf_gemv).
+// Replaces k_rope x2 + k_kv_append + k_attn_decode_split
+// (src/models/transformer.rs:1100-1160).
 template <int D>
 DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                         float* __restrict__ part, unsigned* __restrict__ counters, uint16_t* __restrict__ out,
-                         int q_heads, int kv_heads, int max_seq, int csz, int n_chunks, float theta, float scale,
-                         const int* __restrict__ pos_dev) {
+                         float* __restrict__ part, int q_heads, int kv_heads, int max_seq, int csz, int n_chunks,
+                         float theta, float scale, const int* __restrict__ pos_dev) {
     __shared__ AttnLds<D> L;
     const int t = threadIdx.x;
     const int pos = *pos_dev;
@@ -292,52 +308,41 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
     const int h = blockIdx.x / n_chunks, ci = blockIdx.x % n_chunks;
     const int grp = q_heads / kv_heads, kvh = h / grp;
     const int s0 = ci * csz, s1 = min(s0 + csz, seq);
+    if (s0 >= s1) return;
     const bool has_new = pos < max_seq && s0 <= pos && pos < s1;
-    float* dst = part + ((size_t)h * n_chunks + ci) * (D + 2);
     uint16_t* kh = kc + (size_t)kvh * max_seq * D;
     uint16_t* vh = vc + (size_t)kvh * max_seq * D;
-    if (s0 < s1) {
-        const float p = (float)pos;
-        if (t < D / 2) {
-            const uint16_t* qh = qkv + (size_t)h * D;
-            float oa, ob;
-            rope_rot(h2f(qh[t]), h2f(qh[t + D / 2]), p, t, D, theta, oa, ob);
-            L.q[t] = h2f(f2h(oa));
-            L.q[t + D / 2] = h2f(f2h(ob));
-        } else if (has_new && t < D) {
-            const int i = t - D / 2;
-            const uint16_t* kn = qkv + (size_t)q_heads * D + (size_t)kvh * D;
-            float oa, ob;
-            rope_rot(h2f(kn[i]), h2f(kn[i + D / 2]), p, i, D, theta, oa, ob);
-            const uint32_t ha = f2h(oa), hb = f2h(ob);
-            L.kn[i] = h2f(ha);
-            L.kn[i + D / 2] = h2f(hb);
-            if (h % grp == 0) {
-                kh[(size_t)pos * D + i] = (uint16_t)ha;
-                kh[(size_t)pos * D + i + D / 2] = (uint16_t)hb;
-            }
-        } else if (has_new && t >= D && t < 2 * D) {
-            const int i = t - D;
-            const uint16_t vv = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + i];
-            L.vn[i] = h2f(vv);
-            if (h % grp == 0) vh[(size_t)pos * D + i] = vv;
+    // the chunk's cache loads go out first; the new position's row (not yet
+    // in the cache) is taken from LDS
+    AttnRegs<D> R;
+    attn_issue<D>(R, kh, vh, s0, s1);
+    const float p = (float)pos;
+    if (t < D / 2) {
+        const uint16_t* qh = qkv + (size_t)h * D;
+        float oa, ob;
+        rope_rot(h2f(qh[t]), h2f(qh[t + D / 2]), p, t, D, theta, oa, ob);
+        L.q[t] = h2f(f2h(oa));
+        L.q[t + D / 2] = h2f(f2h(ob));
+    } else if (has_new && t < D) {
+        const int i = t - D / 2;
+        const uint16_t* kn = qkv + (size_t)q_heads * D + (size_t)kvh * D;
+        float oa, ob;
+        rope_rot(h2f(kn[i]), h2f(kn[i + D / 2]), p, i, D, theta, oa, ob);
+        const uint32_t ha = f2h(oa), hb = f2h(ob);
+        L.kn[i] = h2f(ha);
+        L.kn[i + D / 2] = h2f(hb);
+        if (h % grp == 0) {
+            kh[(size_t)pos * D + i] = (uint16_t)ha;
+            kh[(size_t)pos * D + i + D / 2] = (uint16_t)hb;
         }
-        __syncthreads();
-        attn_chunk<D>(L, kh, vh, s0, s1, has_new ? pos : -1, scale, dst);
-    }
-    // publish this chunk's partial, then count it; the last arrival merges
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(&counters[h], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        L.last = prev == (unsigned)(n_chunks - 1);
+    } else if (has_new && t >= D && t < 2 * D) {
+        const int i = t - D;
+        const uint16_t vv = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + i];
+        L.vn[i] = h2f(vv);
+        if (h % grp == 0) vh[(size_t)pos * D + i] = vv;
     }
     __syncthreads();
-    if (!L.last) return;
-    __threadfence();
-    const int active = min((seq + csz - 1) / csz, n_chunks);
-    attn_merge<D>(part + (size_t)h * n_chunks * (D + 2), 0, active, out + (size_t)h * D);
-    if (t == 0) __hip_atomic_store(&counters[h], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    attn_chunk<D>(L, R, s0, s1, has_new ? pos : -1, scale, part + ((size_t)h * n_chunks + ci) * (D + 2));
 }
 
 #define ATTN_KERNELS(D)                                                                                          \
@@ -353,11 +358,9 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
         attn_reduce_body<D>(part, out, csz, n_chunks, seq, max_seq, window, pos_dev);                            \
     }                                                                                                            \
     extern "C" __global__ __launch_bounds__(256) void cima_attn_decode_d##D(                                     \
-        const uint16_t* qkv, uint16_t* kc, uint16_t* vc, float* part, unsigned* counters, uint16_t* out,         \
-        int q_heads, int kv_heads, int max_seq, int csz, int n_chunks, float theta, float scale,                 \
-        const int* pos_dev) {                                                                                    \
-        attn_fused_body<D>(qkv, kc, vc, part, counters, out, q_heads, kv_heads, max_seq, csz, n_chunks, theta,   \
-                           scale, pos_dev);                                                                      \
+        const uint16_t* qkv, uint16_t* kc, uint16_t* vc, float* part, int q_heads, int kv_heads, int max_seq,    \
+        int csz, int n_chunks, float theta, float scale, const int* pos_dev) {                                   \
+        attn_fused_body<D>(qkv, kc, vc, part, q_heads, kv_heads, max_seq, csz, n_chunks, theta, scale, pos_dev); \
     }
 
 ATTN_KERNELS(64)

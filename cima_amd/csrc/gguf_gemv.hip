@@ -5,11 +5,14 @@
 // GEMV's epilogue modes (src/kernels.cu:493-538), for Q8_0, Q4_0, Q4_K and
 // Q6_K weights kept in their GGUF block layout.
 //
-// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair][_epi]
+// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair|_att|_amax][_epi]
 //   R      rows per lane group, ITERS unit steps per row and lane
 //   f32/16 activation, bias and output type
 //   _pair  SwiGLU over a gate and an up weight
+//   _att   x merged from split-attention partials (o projection)
+//   _amax  outputs also reduced into a greedy argmax (head)
 //   _epi   bias and/or residual (mode 1) operands present
+// Every variant can take an RMSNorm prologue (GemvExt::norm_w).
 #include "gguf_formats.h"
 
 // ------------------------------------------------------ reductions (wave64)
@@ -316,6 +319,84 @@ DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, floa
     __syncthreads();
 }
 
+// Optional operands of the fused prologues and epilogues, passed by value.
+struct GemvExt {
+    const void* norm_w;        // RMSNorm prologue weight, or null
+    float eps;
+    int att_chunks;            // attention-merge x source: chunks per head,
+    int att_csz;               //   positions per chunk,
+    int att_dim;               //   head dim,
+    int max_seq;               //   cache length,
+    const int* pos_dev;        //   current position (live length *pos_dev + 1)
+    unsigned long long* slot;  // argmax epilogue target
+};
+
+// Attention-merge x source: x[h*D + d] = f16(sum_c e^(m_c - M) acc_c[d] /
+// sum_c e^(m_c - M) l_c) over the live chunks c of head h, from split
+// attention partials part[(h * chunks + c) * (D + 2)] = {m, l, acc[D]} --
+// the merge of k_attn_reduce (src/kernels.cu:614-639) done by every
+// workgroup of the o-projection that consumes it, into LDS `xt` (fp32).
+// Four neighbouring lanes share a 16-element x chunk, each merging every
+// fourth partial; the four running (M, L, acc) triples then combine.
+DEV void merge_step(float& M, float& L, float a[16], float m2, float l2, const float b[16]) {
+    const float Mn = fmaxf(M, m2);
+    const float s1 = M == -INFINITY ? 0.f : __expf(M - Mn);
+    const float s2 = m2 == -INFINITY ? 0.f : __expf(m2 - Mn);
+    L = L * s1 + l2 * s2;
+#pragma unroll
+    for (int i = 0; i < 16; i++) a[i] = a[i] * s1 + b[i] * s2;
+    M = Mn;
+}
+
+DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, float* xt) {
+    const int D = ext.att_dim, nch = ext.att_chunks, csz = ext.att_csz;
+    const int seq = min(*ext.pos_dev + 1, ext.max_seq);
+    const int active = min((seq + csz - 1) / csz, nch);
+    for (int idx = threadIdx.x; idx < (k >> 2); idx += 256) {
+        const int e0 = (idx >> 2) * 16, sub = idx & 3;
+        const int h = e0 / D, d0 = e0 - h * D;
+        const float* ph = part + (size_t)h * nch * (D + 2);
+        float M = -INFINITY, L = 0.f, a[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) a[i] = 0.f;
+#pragma unroll 2
+        for (int c = sub; c < active; c += 4) {
+            const float* pc = ph + (size_t)c * (D + 2);
+            const float2 ml = *reinterpret_cast<const float2*>(pc);
+            float b[16];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float2 v = reinterpret_cast<const float2*>(pc + 2 + d0)[i];
+                b[2 * i] = v.x;
+                b[2 * i + 1] = v.y;
+            }
+            merge_step(M, L, a, ml.x, ml.y, b);
+        }
+#pragma unroll
+        for (int o = 1; o <= 2; o <<= 1) {
+            const float m2 = __shfl_xor(M, o), l2 = __shfl_xor(L, o);
+            float b[16];
+#pragma unroll
+            for (int i = 0; i < 16; i++) b[i] = __shfl_xor(a[i], o);
+            merge_step(M, L, a, m2, l2, b);
+        }
+        if (sub == 0) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) xt[e0 + i] = h2f(f2h(a[i] / L));
+        }
+    }
+    __syncthreads();
+}
+
+// packed argmax key of an f16 value at index i: orderable f32 bits << 32 | i
+// (k_argmax_softcap without softcap, src/kernels.cu:244-262)
+DEV unsigned long long argmax_key(uint32_t h16, int i) {
+    uint32_t b = __builtin_bit_cast(uint32_t, h2f(h16));
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (uint32_t)i;
+}
+DEV unsigned long long umax64(unsigned long long a, unsigned long long b) { return a > b ? a : b; }
+
 // y[row] = epilogue(W[row,:] . x), rows in [0, n).
 // PAIR = 0: mode 0 -> y = dot (+bias); mode 1 -> y += dot (+bias).
 // PAIR = 1: wa = gate rows, wb = up rows; y = silu(g + bias_a) * (u + bias_b)
@@ -337,11 +418,14 @@ DEV float load_act(const void* p, int i) {
     else return h2f(static_cast<const uint16_t*>(p)[i]);
 }
 
-template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI>
+// XS = 1: x is split-attention partials (stage_attn); AMAX = 1: the f16
+// outputs also feed a greedy argmax into *ext.slot (one u64 atomic max per
+// workgroup).
+template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI, int XS, int AMAX>
 __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ wa,
                           const uint8_t* __restrict__ wb, const void* __restrict__ bias_a,
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
-                          int mode, int lpr_shift, const void* __restrict__ norm_w, float eps) {
+                          int mode, int lpr_shift, const GemvExt& ext) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int S = PAIR ? 2 * R : R;  // weight row streams per lane
     uint8_t* xq = lds;
@@ -410,7 +494,14 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     Slot bufA, bufB;
     issue(bufA, 0);
     // the first row group is in flight while x is staged
-    stage_x<ACT, F::PADSH>(x, k, xq, xs, xsum, norm_w, eps);
+    if constexpr (XS == 1) {
+        float* xt = reinterpret_cast<float*>(lds + ((xstage_bytes<F::PADSH>(k) + 15) & ~15));
+        stage_attn(static_cast<const float*>(x), k, ext, xt);
+        stage_x<ACT_F32, F::PADSH>(xt, k, xq, xs, xsum, nullptr, 0.f);
+    } else {
+        stage_x<ACT, F::PADSH>(x, k, xq, xs, xsum, ext.norm_w, ext.eps);
+    }
+    unsigned long long best = 0ull;
 
     typename F::Xf xreg;
     if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
@@ -456,8 +547,13 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                     }
                 }
                 if (row < n) {
-                    if constexpr (ACT == ACT_F32) static_cast<float*>(y)[row] = out;
-                    else static_cast<uint16_t*>(y)[row] = (uint16_t)f2h(out);
+                    if constexpr (ACT == ACT_F32) {
+                        static_cast<float*>(y)[row] = out;
+                    } else {
+                        const uint32_t hb = f2h(out);
+                        static_cast<uint16_t*>(y)[row] = (uint16_t)hb;
+                        if constexpr (AMAX) best = umax64(best, argmax_key(hb, row));
+                    }
                 }
             }
         }
@@ -471,25 +567,43 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             compute(bufB, i + 1);
         }
     }
+    if constexpr (AMAX) {
+        __shared__ unsigned long long red[4];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const uint32_t lo = __shfl_xor((uint32_t)best, o), hi = __shfl_xor((uint32_t)(best >> 32), o);
+            best = umax64(best, ((unsigned long long)hi << 32) | lo);
+        }
+        if (lane == 0) red[wave] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) atomicMax(ext.slot, umax64(umax64(red[0], red[1]), umax64(red[2], red[3])));
+    }
 }
 
-#define GEMV_KERNEL(NAME, F, R, IT, ACT, PAIR, EPI)                                              \
+#define GEMV_KERNEL(NAME, F, R, IT, ACT, PAIR, EPI, XS, AMAX)                                    \
     extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
         const void* x, const uint8_t* wa, const uint8_t* wb, const void* bias_a,                  \
-        const void* bias_b, void* y, int n, int k, int mode, int lpr_shift, const void* norm_w,   \
-        float eps) {                                                                              \
-        gemv_body<F, R, IT, ACT, PAIR, EPI>(x, wa, wb, bias_a, bias_b, y, n, k, mode, lpr_shift,   \
-                                            norm_w, eps);                                         \
+        const void* bias_b, void* y, int n, int k, int mode, int lpr_shift, GemvExt ext) {       \
+        gemv_body<F, R, IT, ACT, PAIR, EPI, XS, AMAX>(x, wa, wb, bias_a, bias_b, y, n, k, mode,   \
+                                                      lpr_shift, ext);                            \
     }
 
 // name: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair][_epi]
-#define GEMV_EPI(FN, F, R, IT, ACT, AN)                                                   \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN, F, R, IT, ACT, 0, 0)                 \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_epi, F, R, IT, ACT, 0, 1)           \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair, F, R, IT, ACT, 1, 0)          \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair_epi, F, R, IT, ACT, 1, 1)
+#define GEMV_EPI(FN, F, R, IT, ACT, AN)                                                            \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN, F, R, IT, ACT, 0, 0, 0, 0)                    \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_epi, F, R, IT, ACT, 0, 1, 0, 0)              \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair, F, R, IT, ACT, 1, 0, 0, 0)             \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair_epi, F, R, IT, ACT, 1, 1, 0, 0)
 
-#define GEMV_ACT(FN, F, R, IT) GEMV_EPI(FN, F, R, IT, ACT_F32, f32) GEMV_EPI(FN, F, R, IT, ACT_F16, f16)
+// decode-step variants (f16 activations): _att_epi = attention partials as
+// x with bias/residual epilogue (the o projection); _amax = outputs also
+// reduced into a greedy argmax (the head)
+#define GEMV_DECODE(FN, F, R, IT)                                                                  \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_att_epi, F, R, IT, ACT_F16, 0, 1, 1, 0)         \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_amax, F, R, IT, ACT_F16, 0, 0, 0, 1)
+
+#define GEMV_ACT(FN, F, R, IT) GEMV_EPI(FN, F, R, IT, ACT_F32, f32) GEMV_EPI(FN, F, R, IT, ACT_F16, f16) \
+    GEMV_DECODE(FN, F, R, IT)
 
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \

@@ -42,7 +42,7 @@ class DecoderConfig:
     tied: bool = True
     ggml_type: int = gguf.DType.Q8_0
     max_seq: int = 4096
-    attn_chunk: int = 128
+    attn_chunk: int = 256
 
 
 @dataclass
@@ -121,11 +121,9 @@ class DeviceDecoder:
         f16 = torch.float16
         self.x = torch.zeros(c.hidden, dtype=f16, device=dev)
         self.qkv = torch.zeros(qd + 2 * kvd, dtype=f16, device=dev)
-        self.att = torch.zeros(qd, dtype=f16, device=dev)
         self.act = torch.zeros(c.ffn, dtype=f16, device=dev)
         self.logits = torch.zeros(c.vocab, dtype=f16, device=dev)
         self.part = torch.zeros(c.q_heads * n_chunks * (c.head_dim + 2), dtype=torch.float32, device=dev)
-        self.counters = torch.zeros(c.q_heads, dtype=torch.int32, device=dev)
         self.slot = torch.zeros(1, dtype=torch.int64, device=dev)
         self.ids = torch.zeros(1, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -147,8 +145,8 @@ class DeviceDecoder:
             attn_chunk=c.attn_chunk, rope_theta=c.rope_theta, rms_eps=c.rms_eps, embed=p(self.embed),
             head=p(self.head), final_norm=p(self.final_norm),
             layers=ctypes.cast(arr, ctypes.POINTER(DecoderLayer)),
-            x=p(self.x), qkv=p(self.qkv), att=p(self.att), act=p(self.act), logits=p(self.logits),
-            part=p(self.part), counters=p(self.counters), slot=p(self.slot), ids=p(self.ids), pos=p(self.pos))
+            x=p(self.x), qkv=p(self.qkv), act=p(self.act), logits=p(self.logits),
+            part=p(self.part), slot=p(self.slot), ids=p(self.ids), pos=p(self.pos))
 
     def load_kv(self, layer: int, kc: np.ndarray, vc: np.ndarray) -> None:
         L = self.layers[layer]
@@ -168,22 +166,39 @@ class DeviceDecoder:
         self.hip.use_torch_stream()
         self.hip.decode_step(self.desc)
 
-    def capture(self) -> None:
-        """Record one step as a graph (arm_decode_graph); replay() runs it."""
+    def capture(self, native: bool = True) -> None:
+        """Record one step as a graph (arm_decode_graph, src/models/
+        transformer.rs:1467-1497); replay() runs it.  native: the library's
+        own capture of a dedicated stream (cima_hip_capture_begin/end);
+        otherwise torch's CUDAGraph around the same calls."""
         torch = self.torch
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(s):
-            self.hip.set_stream(s)
-            with torch.cuda.graph(g, stream=s):
+        self.stream = s
+        self.hip.set_stream(s)
+        if native:
+            self.hip.capture_begin()
+            try:
                 self.hip.decode_step(self.desc)
+            finally:
+                g = self.hip.capture_end()
+            self.graph = g
+        else:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    self.hip.decode_step(self.desc)
+            self.graph = g
         torch.cuda.current_stream().wait_stream(s)
-        self.hip.use_torch_stream()
-        self.graph = g
 
     def replay(self) -> None:
-        self.graph.replay()
+        """One step: a graph launch on the decoder's stream (self.stream)."""
+        self.hip.set_stream(self.stream)
+        if hasattr(self.graph, "launch"):
+            self.graph.launch()
+        else:
+            with self.torch.cuda.stream(self.stream):
+                self.graph.replay()
 
     def token(self) -> int:
         return int(self.ids.item())

@@ -34,7 +34,9 @@ EXPORTS = (
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
-    "cima_hip_attn_decode", "cima_hip_argmax", "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
+    "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
+    "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
+    "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
 )
 
 
@@ -53,7 +55,7 @@ class Decoder(ctypes.Structure):
         + [(n, ctypes.c_void_p) for n in ("embed", "head", "final_norm")]
         + [("layers", ctypes.POINTER(DecoderLayer))]
         + [(n, ctypes.c_void_p) for n in (
-            "x", "qkv", "att", "act", "logits", "part", "counters", "slot", "ids", "pos")])
+            "x", "qkv", "act", "logits", "part", "slot", "ids", "pos")])
 
 E_INVALID, E_FORMAT, E_NO_KERNEL, E_NOT_INIT = -1, -2, -3, -4
 
@@ -100,11 +102,17 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_kv_append.argtypes = [P, P, P, P, P, I, I, I, I, I, P]
     L.cima_hip_attn_decode_split.argtypes = [P, P, P, P, P, I, I, I, I, I, I, I, F, I, P]
     L.cima_hip_attn_reduce.argtypes = [P, P, P, I, I, I, I, I, I, I, P]
-    L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, P, P, I, I, I, I, I, I, F, F, P]
+    L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, I, I, I, I, I, I, F, F, P]
+    L.cima_hip_attn_gguf_gemv.argtypes = [P, I, P, I, I, I, I, I, P, P, P, P, I, I]
+    L.cima_hip_gguf_gemv_argmax.argtypes = [P, I, P, P, F, P, P, I, I, P]
     L.cima_hip_argmax.argtypes = [P, P, P, I, F]
     L.cima_hip_argmax_to_ids.argtypes = [P, P, P, P]
     L.cima_hip_pos_bump.argtypes = [P, P]
     L.cima_hip_decode_step.argtypes = [P, ctypes.POINTER(Decoder)]
+    L.cima_hip_capture_begin.argtypes = [P]
+    L.cima_hip_capture_end.argtypes = [P, ctypes.POINTER(P)]
+    L.cima_hip_graph_launch.argtypes = [P, P]
+    L.cima_hip_graph_destroy.argtypes = [P]
     L.cima_hip_gguf_gemv_swiglu.argtypes = [P, I, P, P, P, P, P, P, I, I, I]
     L.cima_hip_gguf_gemm.argtypes = [P, I, P, P, P, I, I, I, I, I, I]
     L.cima_hip_gguf_dequant.argtypes = [P, I, P, P, LL]
@@ -277,12 +285,23 @@ class HipCtx:
         self._check(self.lib.cima_hip_attn_reduce(self.handle, _ptr(part), _ptr(out), q_heads, dim, csz, n_chunks,
                                                   seq, max_seq, window, _ptr(pos_dev)))
 
-    def attn_decode(self, qkv, kc, vc, part, counters, out, q_heads: int, kv_heads: int, dim: int, max_seq: int,
-                    csz: int, n_chunks: int, theta: float, scale: float, pos_dev) -> None:
-        """RoPE + KV append + split attention + merge in one launch."""
-        self._check(self.lib.cima_hip_attn_decode(self.handle, _ptr(qkv), _ptr(kc), _ptr(vc), _ptr(part),
-                                                  _ptr(counters), _ptr(out), q_heads, kv_heads, dim, max_seq, csz,
-                                                  n_chunks, theta, scale, _ptr(pos_dev)))
+    def attn_decode(self, qkv, kc, vc, part, q_heads: int, kv_heads: int, dim: int, max_seq: int, csz: int,
+                    n_chunks: int, theta: float, scale: float, pos_dev) -> None:
+        """RoPE + KV append + split attention partials in one launch."""
+        self._check(self.lib.cima_hip_attn_decode(self.handle, _ptr(qkv), _ptr(kc), _ptr(vc), _ptr(part), q_heads,
+                                                  kv_heads, dim, max_seq, csz, n_chunks, theta, scale,
+                                                  _ptr(pos_dev)))
+
+    def attn_gguf_gemv(self, fmt: int, part, q_heads: int, dim: int, csz: int, n_chunks: int, max_seq: int,
+                       pos_dev, w, bias, y, n: int, mode: int = 0) -> None:
+        """o projection of the attention merged from split partials (f16)."""
+        self._check(self.lib.cima_hip_attn_gguf_gemv(self.handle, int(fmt), _ptr(part), q_heads, dim, csz, n_chunks,
+                                                     max_seq, _ptr(pos_dev), _ptr(w), _ptr(bias), _ptr(y), n, mode))
+
+    def gguf_gemv_argmax(self, fmt: int, x, norm_w, eps: float, w, y, n: int, k: int, slot) -> None:
+        """Head GEMV (optional RMSNorm prologue) with the greedy argmax into slot."""
+        self._check(self.lib.cima_hip_gguf_gemv_argmax(self.handle, int(fmt), _ptr(x), _ptr(norm_w), eps, _ptr(w),
+                                                       _ptr(y), n, k, _ptr(slot)))
 
     def argmax(self, x, slot, n: int, cap: float = 0.0) -> None:
         """CudaCtx::argmax_softcap_enqueue (src/cuda.rs:2036); slot must be 0."""
@@ -298,3 +317,36 @@ class HipCtx:
     def decode_step(self, desc: "Decoder") -> None:
         """One greedy decode step of a whole decoder (cima_hip_decode_step)."""
         self._check(self.lib.cima_hip_decode_step(self.handle, ctypes.byref(desc)))
+
+    # -- graphs ---------------------------------------------------------------
+    def capture_begin(self) -> None:
+        """Start recording the context stream (CudaCtx::capture_begin)."""
+        self._check(self.lib.cima_hip_capture_begin(self.handle))
+
+    def capture_end(self) -> "Graph":
+        """Stop recording and instantiate (CudaCtx::capture_end)."""
+        g = ctypes.c_void_p()
+        self._check(self.lib.cima_hip_capture_end(self.handle, ctypes.byref(g)))
+        return Graph(self, g)
+
+
+class Graph:
+    """An instantiated graph of the context's stream; launch() replays it."""
+
+    def __init__(self, ctx: HipCtx, handle):
+        self.ctx = ctx
+        self.handle = handle
+
+    def launch(self) -> None:
+        self.ctx._check(self.ctx.lib.cima_hip_graph_launch(self.ctx.handle, self.handle))
+
+    def close(self) -> None:
+        if getattr(self, "handle", None):
+            self.ctx.lib.cima_hip_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

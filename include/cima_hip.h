@@ -161,7 +161,7 @@ int cima_hip_gguf_gather(cima_hip_ctx* ctx, int ggml_type, const void* table,
  * with the argument meaning of the CudaCtx method it replaces.  pos_dev,
  * where accepted, is a device int holding the current position (graph
  * replay); NULL uses the host value.  Attention needs head_dim 64 or 128,
- * chunk sizes up to 512 and n_chunks * csz >= max_seq.
+ * chunk sizes up to 256 and n_chunks * csz >= max_seq.
  * --------------------------------------------------------------------- */
 
 /* y[r] = f16(sat(x[r]) * rsqrt(mean(sat(x[r])^2) + eps) * w) for rows
@@ -189,17 +189,31 @@ int cima_hip_attn_decode_split(cima_hip_ctx* ctx, const void* q, const void* k_c
  * CudaCtx::attn_reduce (src/cuda.rs:1476-1505). */
 int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_heads, int dim, int csz,
                          int n_chunks, int seq, int max_seq, int window, const int* pos_dev);
-/* One launch for a layer's decode attention at position *pos_dev: RoPE of
- * q and k from qkv = [q | k | v] (the fused q/k/v GEMV output), append of
- * the new k and v to the caches, split attention and merge into out
- * [q_heads, dim].  Replaces rope x2 + kv_append + attn_decode_split +
- * attn_reduce (src/models/transformer.rs:1100-1173).  counters: q_heads
- * unsigned ints, zero before the first call and left zero by every call;
- * part as for the split kernel.  Calls that overlap on one device must not
- * share counters or part. */
-int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* k_cache, void* v_cache, float* part,
-                         unsigned int* counters, void* out, int q_heads, int kv_heads, int dim, int max_seq, int csz,
-                         int n_chunks, float theta, float scale, const int* pos_dev);
+/* One launch for a layer's decode attention partials at position
+ * *pos_dev: RoPE of q and k from qkv = [q | k | v] (the fused q/k/v GEMV
+ * output), append of the new k and v to the caches, and the split
+ * attention of every (query head, chunk) into part (as for
+ * cima_hip_attn_decode_split).  Replaces rope x2 + kv_append +
+ * attn_decode_split (src/models/transformer.rs:1100-1160); the merge is
+ * cima_hip_attn_reduce or, fused, cima_hip_attn_gguf_gemv. */
+int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* k_cache, void* v_cache, float* part, int q_heads,
+                         int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
+                         const int* pos_dev);
+/* The o projection of merged attention: cima_hip_gguf_gemv (f16, mode 0 or
+ * 1, k = q_heads * dim) whose x is merged, inside the GEMV, from the split
+ * partials of the first *pos_dev + 1 positions: x[h*dim + d] =
+ * f16(sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c).  Replaces
+ * attn_reduce + gguf_gemv (src/models/transformer.rs:1161-1238). */
+int cima_hip_attn_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const float* part, int q_heads, int dim, int csz,
+                            int n_chunks, int max_seq, const int* pos_dev, const void* w, const void* bias, void* y,
+                            int n, int mode);
+/* The head GEMV with the greedy argmax folded in: y = W . rmsnorm(x)
+ * (norm_w NULL: W . x), f16, and *slot = max(*slot, argmax key of every
+ * y[r]) with the key of cima_hip_argmax (no softcap).  *slot must be 0 on
+ * entry.  Replaces head_project + argmax_softcap_enqueue
+ * (src/models/transformer.rs:1361-1390, src/cuda.rs:2036-2056). */
+int cima_hip_gguf_gemv_argmax(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* norm_w, float eps,
+                              const void* w, void* y, int n, int k, unsigned long long* slot);
 /* Greedy argmax of f16 logits x[n] (softcap cap > 0: cap * tanh(x / cap))
  * into *slot as (orderable f32 bits << 32 | index), ties to the higher
  * index.  *slot must be 0 on entry (cima_hip_argmax_to_ids leaves it 0).
@@ -232,7 +246,7 @@ typedef struct cima_decoder {
     int embed_type;   /* block format of the embedding table */
     int head_type;    /* block format of head (ignored when tied) */
     int n_layers, hidden, q_heads, kv_heads, head_dim, ffn, vocab, max_seq;
-    int attn_chunk;   /* positions per attention chunk (0 = 128) */
+    int attn_chunk;   /* positions per attention chunk, <= 256 (0 = 256) */
     float rope_theta, rms_eps;
     const void* embed;       /* [vocab, hidden] */
     const void* head;        /* [vocab, hidden], NULL = tied to embed */
@@ -241,11 +255,9 @@ typedef struct cima_decoder {
     /* workspace, all device memory */
     void* x;          /* f16 [hidden] residual stream */
     void* qkv;        /* f16 [(q_heads + 2 kv_heads) * head_dim] */
-    void* att;        /* f16 [q_heads * head_dim] */
     void* act;        /* f16 [ffn] */
     void* logits;     /* f16 [vocab] */
     float* part;      /* q_heads * ceil(max_seq / attn_chunk) * (head_dim + 2) floats */
-    unsigned int* counters;    /* q_heads, zero */
     unsigned long long* slot;  /* zero */
     unsigned int* ids;         /* [1]: input token; receives the greedy next token */
     int* pos;                  /* [1]: position of the input token; advanced by one */
@@ -253,13 +265,27 @@ typedef struct cima_decoder {
 
 /* One greedy batch-1 decode step, all on the context's stream and safe to
  * capture in a HIP graph (positions come from *pos, nothing is allocated):
- * gather ids[0] -> per layer [rmsnorm + q|k|v GEMV + bias, fused attention,
- * o GEMV + residual, rmsnorm + gate|up SwiGLU GEMV, down GEMV + residual]
- * -> rmsnorm + head GEMV -> argmax -> ids[0], pos += 1.  Replaces
+ * gather ids[0] -> per layer [rmsnorm + q|k|v GEMV + bias, RoPE + KV append
+ * + split attention, merge + o GEMV + residual, rmsnorm + gate|up SwiGLU
+ * GEMV, down GEMV + residual] -> rmsnorm + head GEMV + argmax -> ids[0],
+ * pos += 1.  Replaces
  * enqueue_decode_device (src/models/transformer.rs:1440-1461) and
  * forward_chunk_at's rows == 1 path (:1012-1300): 5 launches per layer
  * where the reference issues about 12. */
 int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d);
+
+/* ---------------------------------------------------------------------
+ * Graph capture of the context's stream (CudaCtx::capture_begin /
+ * capture_end / graph_launch, src/cuda.rs:1069-1095): every call between
+ * begin and end is recorded instead of run; the instantiated graph replays
+ * the whole sequence with one launch.  The stream must be a non-default
+ * stream (the context's own, or one set with cima_hip_set_stream).
+ * --------------------------------------------------------------------- */
+typedef struct cima_hip_graph cima_hip_graph;
+int cima_hip_capture_begin(cima_hip_ctx* ctx);
+int cima_hip_capture_end(cima_hip_ctx* ctx, cima_hip_graph** out);
+int cima_hip_graph_launch(cima_hip_ctx* ctx, cima_hip_graph* graph);
+int cima_hip_graph_destroy(cima_hip_graph* graph);
 
 #ifdef __cplusplus
 }

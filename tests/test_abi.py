@@ -48,7 +48,7 @@ def test_code_object_holds_every_kernel():
         blob = blobs["gemv"]
         for r, it in ((1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4)):
             for a in ("f32", "f16"):
-                for sfx in ("", "_epi", "_pair", "_pair_epi"):
+                for sfx in ("", "_epi", "_pair", "_pair_epi") + (("_att_epi", "_amax") if a == "f16" else ()):
                     assert f"cima_gemv_{f}_r{r}_i{it}_{a}{sfx}".encode() in blob
         assert f"cima_dequant_{f}".encode() in blobs["dequant"]
         assert f"cima_gather_{f}".encode() in blobs["dequant"]

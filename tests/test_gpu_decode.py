@@ -175,11 +175,12 @@ def test_attn_split_and_reduce(hip, dim, qh, kvh, seq, csz, window):
             assert np.allclose(P[h, c, 2:], acc, rtol=1e-3, atol=1e-3 * l)
 
 
-@pytest.mark.parametrize("dim,qh,kvh,pos", [(64, 14, 2, 2048), (64, 14, 2, 0), (128, 32, 8, 300),
-                                            (64, 14, 2, 127), (64, 14, 2, 128)])
-def test_attn_decode_fused(hip, dim, qh, kvh, pos):
-    """rope q, k + append + split + merge in one launch == the separate ops."""
-    max_seq, csz = 4096, 128
+@pytest.mark.parametrize("dim,qh,kvh,pos,csz", [(64, 14, 2, 2048, 256), (64, 14, 2, 0, 256), (128, 32, 8, 300, 128),
+                                                (64, 14, 2, 255, 256), (64, 14, 2, 256, 256), (64, 14, 2, 1000, 64)])
+def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz):
+    """rope q, k + append + split in one launch, merged by attn_reduce, ==
+    the separate ops; and the merge folded into the o-projection GEMV."""
+    max_seq = 4096
     nch = max_seq // csz
     r = np.random.default_rng(pos + dim)
     kc = np.zeros((kvh, max_seq, dim), np.float16)
@@ -189,27 +190,34 @@ def test_attn_decode_fused(hip, dim, qh, kvh, pos):
     qkv = (0.5 * r.normal(size=(qh + 2 * kvh) * dim)).astype(np.float16)
     dkc, dvc = dev16(kc), dev16(vc)
     part = torch.zeros(qh * nch * (dim + 2), device="cuda")
-    counters = torch.zeros(qh, dtype=torch.int32, device="cuda")
     out = torch.empty((qh, dim), dtype=torch.float16, device="cuda")
     posd = torch.tensor([pos], dtype=torch.int32, device="cuda")
     scale = 1 / np.sqrt(dim)
-    for rep in range(2):  # counters must come back to zero
-        dkc2, dvc2 = dkc.clone(), dvc.clone()
-        hip.attn_decode(dev16(qkv), dkc2, dvc2, part, counters, out, qh, kvh, dim, max_seq, csz, nch, 1e6, scale,
-                        posd)
-        q = od.rope(qkv[:qh * dim].reshape(1, qh, dim), pos, 1e6)[0]
-        k = od.rope(qkv[qh * dim:(qh + kvh) * dim].reshape(1, kvh, dim), pos, 1e6)
-        v = qkv[(qh + kvh) * dim:].reshape(1, kvh, dim)
-        wk, wv = kc.copy(), vc.copy()
-        od.kv_append(wk, wv, k, v, pos)
-        want = od.attention(q, wk, wv, pos + 1, scale)
-        got = host(out).astype(np.float64)
-        assert np.max(np.abs(got - want)) <= 3e-3, (rep, np.max(np.abs(got - want)))
-        gk = host(dkc2)
-        assert ulps_ok(gk[:, pos], wk[:, pos], ulps=2, atol=2e-4)
-        assert np.all(host(dvc2)[:, pos] == wv[:, pos])
-        assert np.all(gk[:, :pos] == kc[:, :pos]) and np.all(gk[:, pos + 1:] == 0)
-        assert np.all(host(counters) == 0)
+    hip.attn_decode(dev16(qkv), dkc, dvc, part, qh, kvh, dim, max_seq, csz, nch, 1e6, scale, posd)
+    hip.attn_reduce(part, out, qh, dim, csz, nch, 0, max_seq, 0, posd)
+    q = od.rope(qkv[:qh * dim].reshape(1, qh, dim), pos, 1e6)[0]
+    k = od.rope(qkv[qh * dim:(qh + kvh) * dim].reshape(1, kvh, dim), pos, 1e6)
+    v = qkv[(qh + kvh) * dim:].reshape(1, kvh, dim)
+    wk, wv = kc.copy(), vc.copy()
+    od.kv_append(wk, wv, k, v, pos)
+    want = od.attention(q, wk, wv, pos + 1, scale)
+    got = host(out).astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 3e-3, np.max(np.abs(got - want))
+    gk = host(dkc)
+    assert ulps_ok(gk[:, pos], wk[:, pos], ulps=2, atol=2e-4)
+    assert np.all(host(dvc)[:, pos] == wv[:, pos])
+    assert np.all(gk[:, :pos] == kc[:, :pos]) and np.all(gk[:, pos + 1:] == 0)
+    # the same partials merged inside the o projection (mode 1 residual)
+    n = 300
+    w = synth.weights(Q8_0, 40 + dim, 0.02, n, qh * dim)
+    y0 = synth.normal(41, 1.0, n).astype(np.float16)
+    y = dev16(y0)
+    hip.attn_gguf_gemv(Q8_0, part, qh, dim, csz, nch, max_seq, posd, torch.from_numpy(w).cuda(), None, y, n, 1)
+    att = host(out).reshape(-1)  # the merged attention, f16
+    ref = y0.astype(np.float64) + oracle.gguf_gemv_packed(Q8_0, w, att.astype(np.float32), n, qh * dim)
+    r_ = rel(host(y), ref)
+    print(f"attention-merge o GEMV: rel {r_:.2e}")
+    assert r_ <= 1e-3
 
 
 def test_attention_argument_errors(hip):
@@ -241,6 +249,27 @@ def test_argmax_and_feedback(hip, n):
     assert int(host(ids)[0]) == idx and int(host(slot)[0]) == 0 and int(host(pos)[0]) == 42
     hip.pos_bump(pos)
     assert int(host(pos)[0]) == 43
+
+
+@pytest.mark.parametrize("t,n,k", [(Q8_0, 151936, 896), (Q4_K, 5000, 1024), (Q8_0, 3, 64)])
+def test_gemv_argmax(hip, t, n, k):
+    """Head GEMV (+ RMSNorm) with the argmax folded into its epilogue ==
+    the GEMV's own f16 logits fed to the argmax rule."""
+    w = synth.weights(t, 50 + n % 7, 0.02, n, k)
+    x = (2 * synth.normal(51, 1.0, k)).astype(np.float16)
+    g = (1 + synth.normal(52, 0.1, k)).astype(np.float16)
+    y = torch.empty(n, dtype=torch.float16, device="cuda")
+    slot = torch.zeros(1, dtype=torch.int64, device="cuda")
+    hip.gguf_gemv_argmax(t, dev16(x), dev16(g), 1e-6, torch.from_numpy(w).cuda(), y, n, k, slot)
+    logits = host(y)
+    assert int(host(slot).view(np.uint64)[0]) == od.argmax_packed(logits)[1]
+    h = od.rmsnorm(x, g, 1e-6)[0]
+    want = oracle.gguf_gemv_packed(t, w, h.astype(np.float32), n, k, threads=8)
+    assert rel(logits, want) <= 1e-3
+    # without the norm, and a second call into a non-zero slot keeps the max
+    hip.gguf_gemv_argmax(t, dev16(x), None, 0.0, torch.from_numpy(w).cuda(), y, n, k, slot)
+    l2 = host(y)
+    assert int(host(slot).view(np.uint64)[0]) == max(od.argmax_packed(logits)[1], od.argmax_packed(l2)[1])
 
 
 def test_argmax_softcap(hip):
@@ -318,7 +347,7 @@ def test_decode_graph_replay_matches_eager(hip):
         torch.cuda.synchronize()
         assert np.all(host(eager.logits) == host(graph.logits)), s
         assert eager.token() == graph.token() and graph.position() == 101 + s
-        assert np.all(host(graph.counters) == 0)
+        assert int(host(graph.slot)[0]) == 0
 
 
 def test_decode_step_config5_full_size(hip):
