@@ -381,7 +381,13 @@ int cima_hip_bind(cima_hip_ctx* ctx) {
 
 int cima_hip_set_stream(cima_hip_ctx* ctx, void* s) {
     if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_stream: null context");
-    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    ctx->stream = (hipStream_t)s;
+    return 0;
+}
+
+int cima_hip_use_own_stream(cima_hip_ctx* ctx) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_use_own_stream: null context");
+    ctx->stream = ctx->own_stream;
     return 0;
 }
 

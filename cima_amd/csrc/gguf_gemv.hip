@@ -208,9 +208,6 @@ struct IQ6_K {
 template <int PADSH>
 constexpr int xstage_bytes(int k) { return 2 * k + 16 * (k >> PADSH) + 4 * (k >> 5) + 4 * (k >> 4); }
 
-// x -> LDS: thread t takes 16-element chunks t, t+256, ...; the two chunks
-// of a 32-element block sit in neighbouring lanes, which exchange their
-// |x| maxima with one DPP quad permute.
 template <int ACT>
 DEV void load16(const void* __restrict__ x, int c, float v[16]) {
     if constexpr (ACT == ACT_F32) {
@@ -264,50 +261,72 @@ DEV float norm_scale(const void* __restrict__ x, int k, float eps) {
     return 1.0f / sqrtf(tot / (float)k + eps);
 }
 
-// x -> LDS: thread t takes 16-element chunks t, t+256, ...; the two chunks
-// of a 32-element block sit in neighbouring lanes, which exchange their
-// |x| maxima with one DPP quad permute.
-template <int ACT, int PADSH>
-DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, float* xsum,
-                 const void* __restrict__ norm_w, float eps) {
-    const int nchunks = k >> 4;
-    const float inv = norm_w ? norm_scale<ACT>(x, k, eps) : 1.f;
-    for (int c = threadIdx.x; c < nchunks; c += 256) {
-        float v[16];
-        load16<ACT>(x, c, v);
-        if (norm_w) {
-            float g[16];
-            load16<ACT>(norm_w, c, g);
+// x staging.  Thread t owns 16-element chunks base + t + 256 j (j < XB) of
+// every batch; a batch's raw loads are issued together -- for the first
+// batch before the GEMV's first weight row, so x and weights arrive in one
+// round trip -- and held in registers through the RMSNorm reduction.  XB is
+// sized to the row length the kernel variant is built for (ITERS units of
+// every one of up to 64 lanes), so one batch covers x in the common case.
+template <int ACT, int XB>
+struct XBatch {
+    static constexpr int U = ACT == ACT_F32 ? 4 : 2;  // uint4 per chunk
+    uint4 u[XB][U];
+    DEV void load(const void* __restrict__ x, int base, int nck) {
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const float h = sat16(v[i]) * inv * g[i];
-                if constexpr (ACT == ACT_F32) v[i] = h;
-                else v[i] = h2f(f2h(h));
+        for (int j = 0; j < XB; j++) {
+            const int c = min(base + (int)threadIdx.x + 256 * j, nck - 1);
+            const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + (size_t)c * 16 * U);
+#pragma unroll
+            for (int i = 0; i < U; i++) u[j][i] = p[i];
+        }
+    }
+    DEV void get(int j, float v[16]) const {
+#pragma unroll
+        for (int i = 0; i < U; i++) {
+            const uint32_t w[4] = {u[j][i].x, u[j][i].y, u[j][i].z, u[j][i].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if constexpr (ACT == ACT_F32) {
+                    v[4 * i + e] = __builtin_bit_cast(float, w[e]);
+                } else {
+                    v[8 * i + 2 * e] = h2f(w[e] & 0xffffu);
+                    v[8 * i + 2 * e + 1] = h2f(w[e] >> 16);
+                }
             }
         }
-        float amax = 0.f;
+    }
+};
+
+// one chunk -> LDS: 16-bit fixed point split into hi / lo byte planes with
+// the 32-element block's scale; the two chunks of a block sit in
+// neighbouring lanes, which exchange their |x| maxima with one DPP quad
+// permute (both lanes run this, `ok` only gates the stores)
+template <int PADSH>
+DEV void quant_chunk(const float v[16], int c, bool ok, uint8_t* xq, float* xs, float* xsum) {
+    float amax = 0.f;
 #pragma unroll
-        for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
-        amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0xB1, 0xf, 0xf, false)));
-        const float qinv = amax > 0.f ? 32639.f / amax : 0.f;
-        const float scale = amax * (1.0f / 32639.f);
-        uint32_t hw[4], lw[4];
-        int qsum = 0;
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0xB1, 0xf, 0xf, false)));
+    const float qinv = amax > 0.f ? 32639.f / amax : 0.f;
+    const float scale = amax * (1.0f / 32639.f);
+    uint32_t hw[4], lw[4];
+    int qsum = 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            uint32_t hv = 0, lv = 0;
+    for (int i = 0; i < 4; i++) {
+        uint32_t hv = 0, lv = 0;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int q = (int)__builtin_rintf(v[4 * i + j] * qinv);
-                const int hi = (q + 128) >> 8;
-                const int lo = q - (hi << 8);
-                hv |= (uint32_t)(hi & 0xff) << (8 * j);
-                lv |= (uint32_t)(lo & 0xff) << (8 * j);
-                qsum += q;
-            }
-            hw[i] = hv;
-            lw[i] = lv;
+        for (int j = 0; j < 4; j++) {
+            const int q = (int)__builtin_rintf(v[4 * i + j] * qinv);
+            const int hi = (q + 128) >> 8;
+            const int lo = q - (hi << 8);
+            hv |= (uint32_t)(hi & 0xff) << (8 * j);
+            lv |= (uint32_t)(lo & 0xff) << (8 * j);
+            qsum += q;
         }
+        hw[i] = hv;
+        lw[i] = lv;
+    }
+    if (ok) {
         uint4* dst = reinterpret_cast<uint4*>(xq + chunk_off<PADSH>(c));
         dst[0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
         dst[1] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
@@ -315,6 +334,62 @@ DEV void stage_x(const void* __restrict__ x, int k, uint8_t* xq, float* xs, floa
         // on exactly the activations the dot products see
         xsum[c] = scale * (float)qsum;
         if ((c & 1) == 0) xs[c >> 1] = scale;
+    }
+}
+
+// x -> LDS from the first batch already in flight in `xb` (later batches,
+// k > 256 * XB * 16, are loaded here).  With norm_w, x is first replaced by
+// its RMSNorm (sum of squares from the registers when x fits one batch).
+template <int ACT, int XB, int PADSH>
+DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t* xq, float* xs, float* xsum,
+                 const void* __restrict__ norm_w, float eps) {
+    const int nck = k >> 4;
+    const int t = threadIdx.x;
+    float inv = 1.f;
+    if (norm_w) {
+        if (nck <= 256 * XB) {
+            __shared__ float red[4];
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < XB; j++) {
+                float v[16];
+                xb.get(j, v);
+                float sj = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float sv = sat16(v[i]);
+                    sj += sv * sv;
+                }
+                ss += t + 256 * j < nck ? sj : 0.f;
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+            if ((t & 63) == 0) red[t >> 6] = ss;
+            __syncthreads();
+            inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)k + eps);
+        } else {
+            inv = norm_scale<ACT>(x, k, eps);
+        }
+    }
+    for (int base = 0; base < nck; base += 256 * XB) {
+        if (base) xb.load(x, base, nck);
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+            const int c = base + t + 256 * j;
+            float v[16];
+            xb.get(j, v);
+            if (norm_w) {
+                float g[16];
+                load16<ACT>(norm_w, min(c, nck - 1), g);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float h = sat16(v[i]) * inv * g[i];
+                    if constexpr (ACT == ACT_F32) v[i] = h;
+                    else v[i] = h2f(f2h(h));
+                }
+            }
+            quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
+        }
     }
     __syncthreads();
 }
@@ -492,14 +567,21 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     };
 
     Slot bufA, bufB;
-    issue(bufA, 0);
-    // the first row group is in flight while x is staged
+    // x's first batch, then the first row group: both are in flight while
+    // x is staged
+    constexpr int XB = (ITERS * F::UE + 63) / 64 < 4 ? (ITERS * F::UE + 63) / 64 : 4;
     if constexpr (XS == 1) {
+        issue(bufA, 0);
         float* xt = reinterpret_cast<float*>(lds + ((xstage_bytes<F::PADSH>(k) + 15) & ~15));
         stage_attn(static_cast<const float*>(x), k, ext, xt);
-        stage_x<ACT_F32, F::PADSH>(xt, k, xq, xs, xsum, nullptr, 0.f);
+        XBatch<ACT_F32, XB> xb;
+        xb.load(xt, 0, k >> 4);
+        stage_x<ACT_F32, XB, F::PADSH>(xt, k, xb, xq, xs, xsum, nullptr, 0.f);
     } else {
-        stage_x<ACT, F::PADSH>(x, k, xq, xs, xsum, ext.norm_w, ext.eps);
+        XBatch<ACT, XB> xb;
+        xb.load(x, 0, k >> 4);
+        issue(bufA, 0);
+        stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
     }
     unsigned long long best = 0ull;
 
@@ -518,7 +600,15 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             const typename F::Xf& xf = (ITERS == 1) ? xreg : xl;
 #pragma unroll
             for (int s = 0; s < S; s++) {
+#ifdef CIMA_PROBE_NODOT
+                uint32_t wsum = 0;
+                const uint32_t* wp = reinterpret_cast<const uint32_t*>(&cur.w[s][j]);
+#pragma unroll
+                for (int e = 0; e < (int)(sizeof(typename F::Raw) / 4); e++) wsum = wsum * 0x9E3779B1u + wp[e];
+                const float p = (float)wsum;
+#else
                 const float p = F::dot(cur.w[s][j], xf, uu[j]);
+#endif
                 acc[s] += uok[j] ? p : 0.f;
             }
         }
@@ -559,13 +649,14 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         }
     };
 
+    // unconditional issue/compute pairs (steps past `per` re-load the last
+    // row group and write nothing), so every iteration leaves exactly one
+    // row group in flight and the loop head needs no drain
     for (int i = 0; i < per; i += 2) {
         issue(bufB, i + 1);
         compute(bufA, i);
-        if (i + 1 < per) {
-            issue(bufA, i + 2);
-            compute(bufB, i + 1);
-        }
+        issue(bufA, i + 2);
+        compute(bufB, i + 1);
     }
     if constexpr (AMAX) {
         __shared__ unsigned long long red[4];

@@ -28,7 +28,8 @@ CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco") for n in ("gemv", "gemm
 
 # declared in include/cima_hip.h, in order
 EXPORTS = (
-    "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_get_stream",
+    "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_use_own_stream",
+    "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
     "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
@@ -84,6 +85,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_destroy.argtypes = [P]
     L.cima_hip_bind.argtypes = [P]
     L.cima_hip_set_stream.argtypes = [P, P]
+    L.cima_hip_use_own_stream.argtypes = [P]
     L.cima_hip_get_stream.argtypes = [P]
     L.cima_hip_get_stream.restype = P
     L.cima_hip_sync.argtypes = [P]
@@ -181,12 +183,17 @@ class HipCtx:
         self._check(self.lib.cima_hip_bind(self.handle))
 
     def set_stream(self, stream) -> None:
-        """Launch on ``stream`` (a torch stream, a raw hipStream_t, or None
-        for the context's own non-blocking stream)."""
+        """Launch on ``stream``: a torch stream or a raw hipStream_t (0 is
+        the null stream); None returns to the context's own stream."""
+        if stream is None:
+            self._check(self.lib.cima_hip_use_own_stream(self.handle))
+            return
         raw = getattr(stream, "cuda_stream", stream)
-        self._check(self.lib.cima_hip_set_stream(self.handle, raw or None))
+        self._check(self.lib.cima_hip_set_stream(self.handle, raw))
 
     def use_torch_stream(self) -> None:
+        """Launch on torch's current stream of this device (ordered with
+        torch's own kernels there)."""
         import torch
 
         self.set_stream(torch.cuda.current_stream(self.device).cuda_stream)

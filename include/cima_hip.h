@@ -62,9 +62,13 @@ int cima_hip_destroy(cima_hip_ctx* ctx);
  * cuCtxSetCurrent) with hipSetDevice. */
 int cima_hip_bind(cima_hip_ctx* ctx);
 
-/* Launch stream.  NULL restores the context's own non-blocking stream
- * (src/cuda.rs:740-744).  The caller keeps ownership of a stream it sets. */
+/* Launch stream: every later call launches on hip_stream exactly as given
+ * -- NULL is the device's null (legacy default) stream, which orders with
+ * every blocking stream.  The caller keeps ownership of a stream it sets. */
 int cima_hip_set_stream(cima_hip_ctx* ctx, void* hip_stream);
+/* Launches go back to the context's own non-blocking stream, the one the
+ * reference's CudaCtx creates at init (src/cuda.rs:740-744). */
+int cima_hip_use_own_stream(cima_hip_ctx* ctx);
 void* cima_hip_get_stream(cima_hip_ctx* ctx);
 
 /* hipStreamSynchronize on the launch stream: CudaCtx::sync. */

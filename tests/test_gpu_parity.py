@@ -347,3 +347,35 @@ def test_gemv_graph_replay(hip):
         assert np.array_equal(host(yg), eager), i
         hip.gguf_gemv(Q4_K, x, w, None, y, n, k, 0)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_launches_order_with_torch_default_stream(hip):
+    """On torch's default stream the library's kernels are ordered with
+    torch's own: a dependent GEMV pair behind a torch fill of the
+    intermediate never sees the fill (the null stream handle is the null
+    stream, not the context's unsynchronised own stream)."""
+    t = 12
+    w1 = torch.from_numpy(synth.weights(t, 1, 0.02, 2048, 1024)).cuda()
+    w2 = torch.from_numpy(synth.weights(t, 2, 0.02, 512, 2048)).cuda()
+    x = torch.from_numpy(synth.normal(2, 1.0, 1024)).cuda()
+    y1 = torch.empty(2048, device="cuda")
+    hip.use_torch_stream()
+    hip.gguf_gemv(t, x, w1, None, y1, 2048, 1024, 0)
+    ref = torch.empty(512, device="cuda")
+    hip.gguf_gemv(t, y1, w2, None, ref, 512, 2048, 0)
+    torch.cuda.synchronize()
+    outs = [torch.empty(512, device="cuda") for _ in range(16)]
+    for o in outs:
+        y1.fill_(float("nan"))
+        hip.gguf_gemv(t, x, w1, None, y1, 2048, 1024, 0)
+        hip.gguf_gemv(t, y1, w2, None, o, 512, 2048, 0)
+    torch.cuda.synchronize()
+    assert all(torch.equal(o, ref) for o in outs)
+    # the context's own stream, explicitly synchronised, still works
+    hip.set_stream(None)
+    o = torch.empty(512, device="cuda")
+    torch.cuda.synchronize()
+    hip.gguf_gemv(t, y1, w2, None, o, 512, 2048, 0)
+    hip.sync()
+    assert torch.equal(o, ref)
+    hip.use_torch_stream()
