@@ -97,6 +97,7 @@ struct cima_hip_ctx {
     int tune_lpr = 0;
     int tune_wgs = 0;  // workgroups per CU of the persistent grid (0 = built-in default)
     int tune_gemm_bn = 0;  // prefill GEMM token tile (0 = smallest built one covering m)
+    int tune_ring = 0;     // GEMV main loop: 0 = heuristic, 1 = item ring where built, 2 = never
 };
 
 namespace {
@@ -157,12 +158,16 @@ struct GemvExt {
 // extra x source / epilogue of a decode-step GEMV
 enum GemvKind { GK_PLAIN = 0, GK_ATT = 1, GK_AMAX = 2 };
 
+// threads per GEMV workgroup (GNT in gguf_gemv.hip)
+const int kGemvThreads = 256;
+
 struct GemvPlan {
     int rows;        // R: rows per lane group
     int iters;       // unit steps per row and lane
     int lpr_shift;   // log2 of lanes per group (16..64, inside one wave)
-    unsigned grid;   // workgroups of 256 threads
+    unsigned grid;   // workgroups of kGemvThreads threads
     unsigned lds;    // dynamic LDS bytes: x as two int8 planes + padding, scales, sums
+    bool ring;       // item-ring main loop (_ring kernels)
 };
 
 // matches xstage_bytes() in gguf_kernels.hip
@@ -192,12 +197,16 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     int it = 1;
     while (it < iters) it <<= 1;
     int rows = 1;  // measured fastest for every decode shape; 2 is kept for tuning
-    (void)pair;
     if (ctx->tune_rows && have_shape(ctx->tune_rows, it)) rows = ctx->tune_rows;
-    long groups_per_wg = 4L * (64 / lpr);
+    long groups_per_wg = (long)(kGemvThreads / 64) * (64 / lpr);
     long row_groups = ((long)n + rows - 1) / rows;
     long wgs = (row_groups + groups_per_wg - 1) / groups_per_wg;
-    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k)};
+    // the item-ring loop for large matrices of one-unit rows (measured
+    // faster from about 8 MB of weights up; smaller ones are latency-bound
+    // and finish sooner with the plain double buffer)
+    const double wbytes = (double)n * (double)(k / F->block_elems) * F->block_bytes;
+    const bool ring = !pair && rows == 1 && it == 1 && (ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6));
+    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring};
 }
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
@@ -232,6 +241,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
                     p.iters);
     bool epi = ba != nullptr || bb != nullptr || mode == 1;
     const char* kind_sfx = pair ? "_pair" : "";
+    if (kind == GK_ATT) p.ring = false;
     if (kind == GK_ATT) {
         kind_sfx = "_att";
         epi = true;  // built with the epilogue only
@@ -243,16 +253,17 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
         kind_sfx = "_amax";
         if (epi) return fail(CIMA_E_INVALID, "%s: the argmax GEMV takes no bias or residual", api);
     }
-    snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s", F->name, p.rows, p.iters,
-             act == CIMA_DT_F32 ? "f32" : "f16", kind_sfx, epi ? "_epi" : "");
+    snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s%s", F->name, p.rows, p.iters,
+             act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : "", kind_sfx, epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
     int resident = 0;
-    hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, 256, p.lds);
+    hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, kGemvThreads, p.lds);
     if (oe != hipSuccess) return hip_fail(oe, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (resident < 1) resident = 1;
-    // two workgroups per CU measured best for every decode shape on MI355X
-    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : 2;
+    // persistent grid: one workgroup per CU for the item ring and for Q8_0,
+    // two otherwise (measured on MI355X)
+    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : ((p.ring || t == CIMA_GGML_Q8_0) ? 1 : 2);
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;
@@ -267,7 +278,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     ext.eps = eps;
     int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
     void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls, &ext};
-    return launch(ctx, f, p.grid, 256, args, api, p.lds);
+    return launch(ctx, f, p.grid, kGemvThreads, args, api, p.lds);
 }
 
 }  // namespace
@@ -324,6 +335,11 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
                     if (!rc) rc = add(0, name);
                 }
+        for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"}) {
+            char name[96];
+            snprintf(name, sizeof name, "cima_gemv_%s_r1_i1%s", F->name, rk);
+            if (!rc) rc = add(0, name);
+        }
         for (int bn : kGemmBN)
             for (const char* xt : {"f32", "f16", "bf16"})
                 for (const char* yt : {"f32", "f16"}) {
@@ -334,6 +350,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         if (!rc) rc = add(2, std::string("cima_dequant_") + F->name);
         if (!rc) rc = add(2, std::string("cima_gather_") + F->name);
     }
+    if (!rc) rc = add(2, "cima_stream_read");
     for (const char* kn : kDecodeKernels)
         if (!rc) rc = add(3, kn);
     if (rc) {
@@ -351,6 +368,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_ROWS")) er = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_LPR")) el = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -829,6 +847,19 @@ int cima_hip_graph_destroy(cima_hip_graph* g) {
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     delete g;
     return 0;
+}
+
+int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink) {
+    const char* api = "cima_hip_stream_read";
+    if (int rc = ready(ctx, api)) return rc;
+    if (nbytes < 0 || !src || !sink || !aligned(src, 16))
+        return fail(CIMA_E_INVALID, "%s: null or misaligned (16 B) pointer, or nbytes < 0", api);
+    long long n16 = nbytes / 16;
+    if (n16 == 0) return 0;
+    long long grid = (n16 + 4 * 256 - 1) / (4 * 256);
+    if (grid > 4L * ctx->num_cu) grid = 4L * ctx->num_cu;
+    void* args[] = {&src, &n16, &sink};
+    return launch_named(ctx, "cima_stream_read", (unsigned)grid, 256, args, api);
 }
 
 }  // extern "C"

@@ -45,3 +45,21 @@ DQ_KERNELS(q4_0, FQ4_0)
 DQ_KERNELS(q4_k, FQ4_K)
 DQ_KERNELS(q6_k, FQ6_K)
 
+
+// ------------------------------------------------------ bandwidth reference
+// Streams n16 16-byte words once (grid-stride, four independent loads in
+// flight per thread) and folds them into a value that is stored only if it
+// matches an improbable pattern: the plain HBM read ceiling the GEMVs are
+// measured against.
+extern "C" __global__ __launch_bounds__(256) void cima_stream_read(const uint4* __restrict__ src, long long n16,
+                                                                   uint32_t* __restrict__ sink) {
+    const long long nt = (long long)gridDim.x * 256;
+    long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    uint32_t acc = 0;
+    for (; i + 3 * nt < n16; i += 4 * nt) {
+        const uint4 a = src[i], b = src[i + nt], c = src[i + 2 * nt], d = src[i + 3 * nt];
+        acc ^= (a.x + b.y) ^ (c.z + d.w) ^ (a.w + b.x) ^ (c.y + d.z);
+    }
+    for (; i < n16; i += nt) acc ^= src[i].x ^ src[i].w;
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}

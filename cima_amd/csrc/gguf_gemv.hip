@@ -5,12 +5,13 @@
 // GEMV's epilogue modes (src/kernels.cu:493-538), for Q8_0, Q4_0, Q4_K and
 // Q6_K weights kept in their GGUF block layout.
 //
-// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair|_att|_amax][_epi]
+// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_ring][_pair|_att|_amax][_epi]
 //   R      rows per lane group, ITERS unit steps per row and lane
 //   f32/16 activation, bias and output type
 //   _pair  SwiGLU over a gate and an up weight
 //   _att   x merged from split-attention partials (o projection)
 //   _amax  outputs also reduced into a greedy argmax (head)
+//   _ring  item-ring main loop (deeper prefetch; tall one-unit-row matrices)
 //   _epi   bias and/or residual (mode 1) operands present
 // Every variant can take an RMSNorm prologue (GemvExt::norm_w).
 #include "gguf_formats.h"
@@ -203,6 +204,24 @@ struct IQ6_K {
     }
 };
 
+// Workgroup shape: one persistent workgroup of GNW waves per CU (a single
+// dispatch wave of workgroups across the chip; x is staged once per CU).
+constexpr int GNW = 4;
+constexpr int GNT = 64 * GNW;
+
+// sum over the workgroup (every thread calls it; all get the total)
+DEV float block_sum(float v) {
+    __shared__ float red[GNW];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < GNW; w++) t += red[w];
+    return t;
+}
+
 // LDS bytes the GEMV stages for a row length k (x planes + padding, the
 // per-32 scales, the per-16 sums)
 template <int PADSH>
@@ -242,9 +261,8 @@ DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
 // fp32) as the reference's separate rmsnorm launch writes it.
 template <int ACT>
 DEV float norm_scale(const void* __restrict__ x, int k, float eps) {
-    __shared__ float red[4];
     float ss = 0.f;
-    for (int c = threadIdx.x; c < (k >> 4); c += 256) {
+    for (int c = threadIdx.x; c < (k >> 4); c += GNT) {
         float v[16];
         load16<ACT>(x, c, v);
 #pragma unroll
@@ -253,15 +271,10 @@ DEV float norm_scale(const void* __restrict__ x, int k, float eps) {
             ss += s * s;
         }
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    return 1.0f / sqrtf(tot / (float)k + eps);
+    return 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
 }
 
-// x staging.  Thread t owns 16-element chunks base + t + 256 j (j < XB) of
+// x staging.  Thread t owns 16-element chunks base + t + GNT j (j < XB) of
 // every batch; a batch's raw loads are issued together -- for the first
 // batch before the GEMV's first weight row, so x and weights arrive in one
 // round trip -- and held in registers through the RMSNorm reduction.  XB is
@@ -274,7 +287,7 @@ struct XBatch {
     DEV void load(const void* __restrict__ x, int base, int nck) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
-            const int c = min(base + (int)threadIdx.x + 256 * j, nck - 1);
+            const int c = min(base + (int)threadIdx.x + GNT * j, nck - 1);
             const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + (size_t)c * 16 * U);
 #pragma unroll
             for (int i = 0; i < U; i++) u[j][i] = p[i];
@@ -347,8 +360,7 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
     const int t = threadIdx.x;
     float inv = 1.f;
     if (norm_w) {
-        if (nck <= 256 * XB) {
-            __shared__ float red[4];
+        if (nck <= GNT * XB) {
             float ss = 0.f;
 #pragma unroll
             for (int j = 0; j < XB; j++) {
@@ -360,22 +372,18 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
                     const float sv = sat16(v[i]);
                     sj += sv * sv;
                 }
-                ss += t + 256 * j < nck ? sj : 0.f;
+                ss += t + GNT * j < nck ? sj : 0.f;
             }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-            if ((t & 63) == 0) red[t >> 6] = ss;
-            __syncthreads();
-            inv = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / (float)k + eps);
+            inv = 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
         } else {
             inv = norm_scale<ACT>(x, k, eps);
         }
     }
-    for (int base = 0; base < nck; base += 256 * XB) {
+    for (int base = 0; base < nck; base += GNT * XB) {
         if (base) xb.load(x, base, nck);
 #pragma unroll
         for (int j = 0; j < XB; j++) {
-            const int c = base + t + 256 * j;
+            const int c = base + t + GNT * j;
             float v[16];
             xb.get(j, v);
             if (norm_w) {
@@ -393,6 +401,11 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
     }
     __syncthreads();
 }
+
+#ifdef CIMA_PROBE_TIMES
+// per-workgroup timestamps of an instrumented build (never in the product)
+__device__ unsigned long long g_probe_ts[8192 * 16];
+#endif
 
 // Optional operands of the fused prologues and epilogues, passed by value.
 struct GemvExt {
@@ -427,7 +440,7 @@ DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, f
     const int D = ext.att_dim, nch = ext.att_chunks, csz = ext.att_csz;
     const int seq = min(*ext.pos_dev + 1, ext.max_seq);
     const int active = min((seq + csz - 1) / csz, nch);
-    for (int idx = threadIdx.x; idx < (k >> 2); idx += 256) {
+    for (int idx = threadIdx.x; idx < (k >> 2); idx += GNT) {
         const int e0 = (idx >> 2) * 16, sub = idx & 3;
         const int h = e0 / D, d0 = e0 - h * D;
         const float* ph = part + (size_t)h * nch * (D + 2);
@@ -496,12 +509,15 @@ DEV float load_act(const void* p, int i) {
 // XS = 1: x is split-attention partials (stage_attn); AMAX = 1: the f16
 // outputs also feed a greedy argmax into *ext.slot (one u64 atomic max per
 // workgroup).
-template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI, int XS, int AMAX>
+template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI, int XS, int AMAX, int RING>
 __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ wa,
                           const uint8_t* __restrict__ wb, const void* __restrict__ bias_a,
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
                           int mode, int lpr_shift, const GemvExt& ext) {
     extern __shared__ __align__(16) uint8_t lds[];
+#ifdef CIMA_PROBE_TIMES
+    if (threadIdx.x == 0) g_probe_ts[blockIdx.x * 16] = __builtin_amdgcn_s_memrealtime();
+#endif
     constexpr int S = PAIR ? 2 * R : R;  // weight row streams per lane
     uint8_t* xq = lds;
     float* xs = reinterpret_cast<float*>(lds + 2 * k + 16 * (k >> F::PADSH));
@@ -517,9 +533,9 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     // contiguous window of the weight; every wave runs `per` steps (the
     // count of its first group) and a group's extra step re-loads (and does
     // not write) its own last row group
-    const int ngroups = gridDim.x * 4 * gpw;
-    const int gid = (blockIdx.x * 4 + wave) * gpw + (lane >> lpr_shift);
-    const int gid0 = (blockIdx.x * 4 + wave) * gpw;
+    const int ngroups = gridDim.x * GNW * gpw;
+    const int gid = (blockIdx.x * GNW + wave) * gpw + (lane >> lpr_shift);
+    const int gid0 = (blockIdx.x * GNW + wave) * gpw;
     const int per = gid0 < nrg ? (nrg - 1 - gid0) / ngroups + 1 : 0;
     const int cnt = gid < nrg ? (nrg - 1 - gid) / ngroups + 1 : 0;
     const int rg_last = cnt > 0 ? gid + (cnt - 1) * ngroups : nrg - 1;  // clamp target of loads
@@ -543,78 +559,34 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     const void* p1 = has1 ? bias_a : x;
     const void* p2 = has2 ? (PAIR ? bias_b : static_cast<const void*>(y)) : x;
 
-    struct Slot {
-        typename F::Raw w[S][ITERS];
-        float e1[R], e2[R];
-    };
-    auto issue = [&](Slot& dst, int i) {
-        const int g = min(gid + i * ngroups, rg_last);
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            const int row = min(g * R + (s % R), n - 1);
-            const uint8_t* rp = ((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes;
-#pragma unroll
-            for (int j = 0; j < ITERS; j++) dst.w[s][j] = F::load(rp, uu[j]);
+    // x chunks per thread for the longest row this variant serves (ITERS
+    // units of 64 lanes): k / 16 / GNT
+    constexpr int XB = (ITERS * F::UE * 4 + GNT - 1) / GNT;
+    // x -> LDS; the caller has the first weights in flight (and, for plain
+    // x, x's first batch ahead of them in `xb`)
+    auto stage = [&](XBatch<ACT, XB>& xb) {
+        if constexpr (XS == 1) {
+            float* xt = reinterpret_cast<float*>(lds + ((xstage_bytes<F::PADSH>(k) + 15) & ~15));
+            stage_attn(static_cast<const float*>(x), k, ext, xt);
+            XBatch<ACT_F32, XB> xa;
+            xa.load(xt, 0, k >> 4);
+            stage_x<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
+        } else {
+            stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
         }
-        if constexpr (EPI) {
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const int erow = min(g * R + r, n - 1);
-                dst.e1[r] = load_act<ACT>(p1, has1 ? erow : 0);
-                dst.e2[r] = load_act<ACT>(p2, has2 ? erow : 0);
-            }
-        }
-    };
-
-    Slot bufA, bufB;
-    // x's first batch, then the first row group: both are in flight while
-    // x is staged
-    constexpr int XB = (ITERS * F::UE + 63) / 64 < 4 ? (ITERS * F::UE + 63) / 64 : 4;
-    if constexpr (XS == 1) {
-        issue(bufA, 0);
-        float* xt = reinterpret_cast<float*>(lds + ((xstage_bytes<F::PADSH>(k) + 15) & ~15));
-        stage_attn(static_cast<const float*>(x), k, ext, xt);
-        XBatch<ACT_F32, XB> xb;
-        xb.load(xt, 0, k >> 4);
-        stage_x<ACT_F32, XB, F::PADSH>(xt, k, xb, xq, xs, xsum, nullptr, 0.f);
-    } else {
-        XBatch<ACT, XB> xb;
-        xb.load(x, 0, k >> 4);
-        issue(bufA, 0);
-        stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
-    }
-    unsigned long long best = 0ull;
-
-    typename F::Xf xreg;
-    if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
-
-    auto compute = [&](const Slot& cur, int i) {
-        const int rg = gid + i * ngroups;
-        float acc[S];
-#pragma unroll
-        for (int s = 0; s < S; s++) acc[s] = 0.f;
-#pragma unroll
-        for (int j = 0; j < ITERS; j++) {
-            typename F::Xf xl;
-            if constexpr (ITERS != 1) F::loadx(xq, xs, xsum, uu[j], xl);
-            const typename F::Xf& xf = (ITERS == 1) ? xreg : xl;
-#pragma unroll
-            for (int s = 0; s < S; s++) {
-#ifdef CIMA_PROBE_NODOT
-                uint32_t wsum = 0;
-                const uint32_t* wp = reinterpret_cast<const uint32_t*>(&cur.w[s][j]);
-#pragma unroll
-                for (int e = 0; e < (int)(sizeof(typename F::Raw) / 4); e++) wsum = wsum * 0x9E3779B1u + wp[e];
-                const float p = (float)wsum;
-#else
-                const float p = F::dot(cur.w[s][j], xf, uu[j]);
+#ifdef CIMA_PROBE_TIMES
+        if (threadIdx.x == 0) g_probe_ts[blockIdx.x * 16 + 1] = __builtin_amdgcn_s_memrealtime();
 #endif
-                acc[s] += uok[j] ? p : 0.f;
-            }
-        }
+    };
+    unsigned long long best = 0ull;
+    typename F::Xf xreg;
+
+    // reduce a row group's per-lane partial sums over the lane group; its
+    // last lane applies the epilogue and writes the R rows of group i
+    auto finish = [&](float (&acc)[S], const float* e1, const float* e2, int i) {
 #pragma unroll
         for (int s = 0; s < S; s++) acc[s] = group_sum_last(acc[s], 1 << lpr_shift);
-        // the group's last lane holds the R row totals and writes them
+        const int rg = gid + i * ngroups;
         if (li == (1 << lpr_shift) - 1 && i < cnt) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
@@ -622,18 +594,18 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                 float v = acc[r];
                 float out;
                 if constexpr (EPI) {
-                    if (has1) v += cur.e1[r];
+                    if (has1) v += e1[r];
                 }
                 if constexpr (PAIR) {
                     float v2 = acc[R + r];
                     if constexpr (EPI) {
-                        if (has2) v2 += cur.e2[r];
+                        if (has2) v2 += e2[r];
                     }
                     out = (v / (1.0f + __expf(-v))) * v2;
                 } else {
                     out = v;
                     if constexpr (EPI) {
-                        if (has2) out += cur.e2[r];
+                        if (has2) out += e2[r];
                     }
                 }
                 if (row < n) {
@@ -648,18 +620,121 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             }
         }
     };
+    auto epi_load = [&](float* e1, float* e2, int g) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int erow = min(g * R + r, n - 1);
+            e1[r] = load_act<ACT>(p1, has1 ? erow : 0);
+            e2[r] = load_act<ACT>(p2, has2 ? erow : 0);
+        }
+    };
+    auto wdot = [&](const typename F::Raw& w, const typename F::Xf& xf, int u) -> float {
+#ifdef CIMA_PROBE_NODOT
+        uint32_t wsum = 0;
+        const uint32_t* wp = reinterpret_cast<const uint32_t*>(&w);
+#pragma unroll
+        for (int e = 0; e < (int)(sizeof(typename F::Raw) / 4); e++) wsum = wsum * 0x9E3779B1u + wp[e];
+        return (float)wsum;
+#else
+        return F::dot(w, xf, u);
+#endif
+    };
 
-    // unconditional issue/compute pairs (steps past `per` re-load the last
-    // row group and write nothing), so every iteration leaves exactly one
-    // row group in flight and the loop head needs no drain
-    for (int i = 0; i < per; i += 2) {
-        issue(bufB, i + 1);
-        compute(bufA, i);
-        issue(bufA, i + 2);
-        compute(bufB, i + 1);
+    if constexpr (RING) {
+        // Item ring (single-row, one-unit-per-lane rows): item q is the
+        // lane's q-th row group; DEPTH items are in flight in a ring of
+        // slots and the loop body is unrolled over DEPTH items so slot
+        // indices are compile-time constants.  Items past the lane's last
+        // row group re-load that row group (a cache hit) and write nothing.
+        static_assert(ITERS == 1, "the item ring serves one-unit rows");
+        constexpr int DEPTH = S >= 2 ? 2 : 4;
+        struct Item {
+            typename F::Raw w[S];
+            float e1[R], e2[R];
+        };
+        auto issue = [&](Item& dst, int q) {
+            const int g = min(gid + q * ngroups, rg_last);
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int row = min(g * R + (s % R), n - 1);
+                dst.w[s] = F::load(((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes, uu[0]);
+            }
+            if constexpr (EPI) epi_load(dst.e1, dst.e2, g);
+        };
+        Item ring[DEPTH];
+        XBatch<ACT, XB> xb;
+        if constexpr (XS == 0) xb.load(x, 0, k >> 4);
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
+        stage(xb);
+        F::loadx(xq, xs, xsum, uu[0], xreg);
+        for (int base = 0; base < per; base += DEPTH) {
+#pragma unroll
+            for (int b = 0; b < DEPTH; b++) {
+                float acc[S];
+#pragma unroll
+                for (int s = 0; s < S; s++) acc[s] = uok[0] ? wdot(ring[b].w[s], xreg, uu[0]) : 0.f;
+                finish(acc, ring[b].e1, ring[b].e2, base + b);
+                issue(ring[b], base + b + DEPTH);
+            }
+        }
+    } else {
+        // Row-group double buffer: a lane holds all ITERS units of a row
+        // group; the next row group is loaded while the current one is
+        // computed.  Loads are never predicated (a group's extra step
+        // re-loads its own last row group, a cache hit) and issue/compute
+        // alternate unconditionally, so every loop iteration leaves exactly
+        // one row group in flight and the loop head needs no drain.
+        struct Slot {
+            typename F::Raw w[S][ITERS];
+            float e1[R], e2[R];
+        };
+        auto issue = [&](Slot& dst, int i) {
+            const int g = min(gid + i * ngroups, rg_last);
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int row = min(g * R + (s % R), n - 1);
+                const uint8_t* rp = ((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes;
+#pragma unroll
+                for (int j = 0; j < ITERS; j++) dst.w[s][j] = F::load(rp, uu[j]);
+            }
+            if constexpr (EPI) epi_load(dst.e1, dst.e2, g);
+        };
+        auto compute = [&](const Slot& cur, int i) {
+            float acc[S];
+#pragma unroll
+            for (int s = 0; s < S; s++) acc[s] = 0.f;
+#pragma unroll
+            for (int j = 0; j < ITERS; j++) {
+                typename F::Xf xl;
+                if constexpr (ITERS != 1) F::loadx(xq, xs, xsum, uu[j], xl);
+                const typename F::Xf& xf = (ITERS == 1) ? xreg : xl;
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    const float p = wdot(cur.w[s][j], xf, uu[j]);
+                    acc[s] += uok[j] ? p : 0.f;
+                }
+            }
+            finish(acc, cur.e1, cur.e2, i);
+        };
+        Slot bufA, bufB;
+        XBatch<ACT, XB> xb;
+        if constexpr (XS == 0) xb.load(x, 0, k >> 4);
+        issue(bufA, 0);
+        stage(xb);
+        if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
+        for (int i = 0; i < per; i += 2) {
+            issue(bufB, i + 1);
+            compute(bufA, i);
+            issue(bufA, i + 2);
+            compute(bufB, i + 1);
+        }
     }
+#ifdef CIMA_PROBE_TIMES
+    if (lane == 0) g_probe_ts[blockIdx.x * 16 + 2 + wave] = __builtin_amdgcn_s_memrealtime();
+#endif
     if constexpr (AMAX) {
-        __shared__ unsigned long long red[4];
+        __shared__ unsigned long long red[GNW];
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) {
             const uint32_t lo = __shfl_xor((uint32_t)best, o), hi = __shfl_xor((uint32_t)(best >> 32), o);
@@ -667,39 +742,53 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         }
         if (lane == 0) red[wave] = best;
         __syncthreads();
-        if (threadIdx.x == 0) atomicMax(ext.slot, umax64(umax64(red[0], red[1]), umax64(red[2], red[3])));
+        if (threadIdx.x == 0) {
+            unsigned long long m = 0ull;
+#pragma unroll
+            for (int w = 0; w < GNW; w++) m = umax64(m, red[w]);
+            atomicMax(ext.slot, m);
+        }
     }
 }
 
-#define GEMV_KERNEL(NAME, F, R, IT, ACT, PAIR, EPI, XS, AMAX)                                    \
-    extern "C" __global__ __launch_bounds__(256) void NAME(                                       \
+#define GEMV_KERNEL(NAME, F, R, IT, ACT, PAIR, EPI, XS, AMAX, RING)                              \
+    extern "C" __global__ __launch_bounds__(GNT) void NAME(                                       \
         const void* x, const uint8_t* wa, const uint8_t* wb, const void* bias_a,                  \
         const void* bias_b, void* y, int n, int k, int mode, int lpr_shift, GemvExt ext) {       \
-        gemv_body<F, R, IT, ACT, PAIR, EPI, XS, AMAX>(x, wa, wb, bias_a, bias_b, y, n, k, mode,   \
-                                                      lpr_shift, ext);                            \
+        gemv_body<F, R, IT, ACT, PAIR, EPI, XS, AMAX, RING>(x, wa, wb, bias_a, bias_b, y, n, k,   \
+                                                            mode, lpr_shift, ext);                \
     }
 
 // name: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_pair][_epi]
-#define GEMV_EPI(FN, F, R, IT, ACT, AN)                                                            \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN, F, R, IT, ACT, 0, 0, 0, 0)                    \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_epi, F, R, IT, ACT, 0, 1, 0, 0)              \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair, F, R, IT, ACT, 1, 0, 0, 0)             \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair_epi, F, R, IT, ACT, 1, 1, 0, 0)
+#define GEMV_EPI(FN, F, R, IT, ACT, AN)                                                               \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN, F, R, IT, ACT, 0, 0, 0, 0, 0)                    \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_epi, F, R, IT, ACT, 0, 1, 0, 0, 0)              \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair, F, R, IT, ACT, 1, 0, 0, 0, 0)             \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_##AN##_pair_epi, F, R, IT, ACT, 1, 1, 0, 0, 0)
 
 // decode-step variants (f16 activations): _att_epi = attention partials as
 // x with bias/residual epilogue (the o projection); _amax = outputs also
 // reduced into a greedy argmax (the head)
-#define GEMV_DECODE(FN, F, R, IT)                                                                  \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_att_epi, F, R, IT, ACT_F16, 0, 1, 1, 0)         \
-    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_amax, F, R, IT, ACT_F16, 0, 0, 0, 1)
+#define GEMV_DECODE(FN, F, R, IT)                                                                     \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_att_epi, F, R, IT, ACT_F16, 0, 1, 1, 0, 0)         \
+    GEMV_KERNEL(cima_gemv_##FN##_r##R##_i##IT##_f16_amax, F, R, IT, ACT_F16, 0, 0, 0, 1, 0)
 
 #define GEMV_ACT(FN, F, R, IT) GEMV_EPI(FN, F, R, IT, ACT_F32, f32) GEMV_EPI(FN, F, R, IT, ACT_F16, f16) \
     GEMV_DECODE(FN, F, R, IT)
 
+// item-ring variants (one row, one unit per lane; tall matrices):
+// cima_gemv_<fmt>_r1_i1_<f32|f16>_ring[_epi], cima_gemv_<fmt>_r1_i1_f16_ring_amax
+#define GEMV_RING(FN, F)                                                                              \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f32_ring, F, 1, 1, ACT_F32, 0, 0, 0, 0, 1)                       \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f32_ring_epi, F, 1, 1, ACT_F32, 0, 1, 0, 0, 1)                   \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring, F, 1, 1, ACT_F16, 0, 0, 0, 0, 1)                       \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring_epi, F, 1, 1, ACT_F16, 0, 1, 0, 0, 1)                   \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring_amax, F, 1, 1, ACT_F16, 0, 0, 0, 1, 1)
+
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \
     GEMV_ACT(FN, F, 1, 1) GEMV_ACT(FN, F, 1, 2) GEMV_ACT(FN, F, 1, 4) GEMV_ACT(FN, F, 1, 8)   \
-    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4)
+    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F)
 
 GEMV_FMT(q8_0, IQ8_0)
 GEMV_FMT(q4_0, IQ4_0)

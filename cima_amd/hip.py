@@ -38,6 +38,7 @@ EXPORTS = (
     "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
     "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
+    "cima_hip_stream_read",
 )
 
 
@@ -112,6 +113,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_pos_bump.argtypes = [P, P]
     L.cima_hip_decode_step.argtypes = [P, ctypes.POINTER(Decoder)]
     L.cima_hip_capture_begin.argtypes = [P]
+    L.cima_hip_stream_read.argtypes = [P, P, LL, P]
     L.cima_hip_capture_end.argtypes = [P, ctypes.POINTER(P)]
     L.cima_hip_graph_launch.argtypes = [P, P]
     L.cima_hip_graph_destroy.argtypes = [P]
@@ -324,6 +326,10 @@ class HipCtx:
     def decode_step(self, desc: "Decoder") -> None:
         """One greedy decode step of a whole decoder (cima_hip_decode_step)."""
         self._check(self.lib.cima_hip_decode_step(self.handle, ctypes.byref(desc)))
+
+    def stream_read(self, src, nbytes: int, sink) -> None:
+        """Read nbytes once (bandwidth reference)."""
+        self._check(self.lib.cima_hip_stream_read(self.handle, _ptr(src), nbytes, _ptr(sink)))
 
     # -- graphs ---------------------------------------------------------------
     def capture_begin(self) -> None:

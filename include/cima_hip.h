@@ -88,11 +88,12 @@ int cima_hip_num_cu(cima_hip_ctx* ctx);
  * (1 or 2) and lanes per group (16..256, a power of two) for every
  * later gguf_gemv call on this context; 0 restores the built-in heuristic.
  * The environment variables CIMA_GEMV_ROWS / CIMA_GEMV_LPR set the initial
- * values at cima_hip_init. */
+ * values at cima_hip_init (CIMA_GEMV_RING=1 / 2 forces / forbids the
+ * item-ring main loop for one-unit rows). */
 int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
 
 /* GEMV grid tuning (no counterpart in the reference): the persistent grid
- * holds at most this many workgroups per CU (0 = the default of 2, or fewer
+ * holds at most this many 256-thread workgroups per CU (0 = the default of 1, or fewer
  * if fewer fit; environment variable CIMA_GEMV_WGS at init). */
 int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
@@ -290,6 +291,12 @@ int cima_hip_capture_begin(cima_hip_ctx* ctx);
 int cima_hip_capture_end(cima_hip_ctx* ctx, cima_hip_graph** out);
 int cima_hip_graph_launch(cima_hip_ctx* ctx, cima_hip_graph* graph);
 int cima_hip_graph_destroy(cima_hip_graph* graph);
+
+/* Bandwidth reference (no counterpart in the reference): reads nbytes
+ * (16-byte aligned src, whole 16-byte words) once with plain streaming
+ * loads; *sink is written only in an improbable case.  The HBM read rate a
+ * kernel can reach, measured the way the GEMVs are. */
+int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink);
 
 #ifdef __cplusplus
 }

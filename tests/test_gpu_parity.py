@@ -379,3 +379,39 @@ def test_launches_order_with_torch_default_stream(hip):
     hip.sync()
     assert torch.equal(o, ref)
     hip.use_torch_stream()
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
+def test_item_ring_matches_double_buffer(t):
+    """The item-ring main loop (forced on with CIMA_GEMV_RING=1, forced off
+    with 2) computes every row exactly as the row-group double buffer does:
+    identical outputs, f32 and f16, with and without the epilogue."""
+    import os
+    from cima_amd.hip import HipCtx
+
+    ctxs = {}
+    for mode in ("1", "2"):
+        os.environ["CIMA_GEMV_RING"] = mode
+        try:
+            ctxs[mode] = HipCtx(0)
+        finally:
+            del os.environ["CIMA_GEMV_RING"]
+        ctxs[mode].use_torch_stream()
+    be = {2: 32, 8: 32, 12: 256, 14: 256}[t]
+    k = 64 * (64 if be == 256 else 32) // 2  # one unit per lane at 32 lanes
+    for n in (1, 37, 1000):
+        w = torch.from_numpy(synth.weights(t, 80 + n, 0.02, n, k)).cuda()
+        for dt in (torch.float32, torch.float16):
+            x = torch.from_numpy(synth.normal(81, 1.0, k)).to(dt).cuda()
+            b = torch.from_numpy(synth.normal(82, 0.1, n)).to(dt).cuda()
+            outs = []
+            for mode, c in ctxs.items():
+                y = torch.from_numpy(synth.normal(83, 1.0, n)).to(dt).cuda()
+                c.gguf_gemv(t, x, w, b, y, n, k, 1)
+                y0 = torch.empty(n, dtype=dt, device="cuda")
+                c.gguf_gemv(t, x, w, None, y0, n, k, 0)
+                outs.append((y, y0))
+            torch.cuda.synchronize()
+            assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (n, dt)
+    for c in ctxs.values():
+        c.close()
