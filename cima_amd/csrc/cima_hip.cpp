@@ -516,7 +516,9 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
     if (!aligned(x, 8) || !aligned(w, F->w_align) || !aligned(y, 4))
         return fail(CIMA_E_INVALID, "%s: misaligned pointer (x 8 B, %s weights %d B, y 4 B)", api, F->name,
                     F->w_align);
-    // token tile: the smallest built width covering m, else 128
+    // token tile: the smallest built width covering m, else 128; the
+    // 16-token tile stages 128 k at a time (64-row weight tiles), so it
+    // needs k % 128 == 0
     int bn = 128;
     for (int b : kGemmBN)
         if (m <= b) {
@@ -524,6 +526,8 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
             break;
         }
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
+    if (bn == 16 && k % 128) bn = 64;
+    const int bm = bn == 16 ? 64 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];
     snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xn[x_dtype], y_dtype == CIMA_DT_F32 ? "f32" : "f16");
@@ -534,7 +538,7 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
     void* ya = y;
     int mm = m, nn = n, kk = k, ld = ldy;
     void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
-    hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + 127) / 128), (unsigned)((m + bn - 1) / bn), 1, 256, 1, 1,
+    hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, 256, 1, 1,
                                          0, ctx->stream, args, nullptr);
     return e == hipSuccess ? 0 : hip_fail(e, api);
 }

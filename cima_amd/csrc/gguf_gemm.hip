@@ -5,13 +5,14 @@
 // Y[m, n] (row stride ldy) = X[m, k] . W[n, k]^T: X holds m tokens, W is the
 // packed GGUF weight (the engine's lin_gemm, src/models/transformer.rs:
 // 618-655, which dequantises W to an f16 slab and runs an f16 GEMM).
-// Each stage of 64 k, a 256-thread workgroup dequantises its 128 weight
-// rows x 64 k to f16 in LDS -- bit-exact with the host decoders, so the
-// operand equals the reference's dequantised weight -- stages the X tile as
-// f16 (bf16 -> f16 is exact for |x| >= 2^-14), and runs
-// v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Wave w owns weight rows
-// [32w, 32w+32) of the tile and all BN tokens.  LDS is double-buffered: the
-// global loads of stage s+1 are in flight while stage s is multiplied.
+// Each stage (BM weight rows x BK k, 8192 weights), a 256-thread workgroup
+// dequantises its weights to f16 in LDS -- bit-exact with the host
+// decoders, so the operand equals the reference's dequantised weight --
+// stages the X tile as f16 (bf16 -> f16 is exact for |x| >= 2^-14), and
+// runs v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Wave w owns weight
+// rows [w BM/4, (w+1) BM/4) of the tile and all BN tokens.  LDS is
+// double-buffered; the global loads of the next PF stages are in flight in
+// registers while a stage is multiplied.
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -116,106 +117,140 @@ struct DQ6_K {
     }
 };
 
-constexpr int GBM = 128;        // weight rows per workgroup
-constexpr int GBK = 64;         // k per stage
-constexpr int GKP = GBK + 8;    // LDS row pitch in halves (pads away bank conflicts)
+// x element pairs (i, i+1) as loaded (f16 / bf16: one dword, f32: two), and
+// their conversion to packed f16 -- done when the stage is consumed, so the
+// loads stay in flight
+template <int XT> struct XPair { using T = uint32_t; };
+template <> struct XPair<XT_F32> { using T = float2; };
 
 template <int XT>
-DEV uint32_t x_pair_f16(const void* x, size_t i) {  // elements i, i+1 -> packed f16
+DEV typename XPair<XT>::T x_pair_load(const void* x, size_t i) {
+    if constexpr (XT == XT_F32) return *reinterpret_cast<const float2*>(static_cast<const float*>(x) + i);
+    else return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
+}
+
+template <int XT>
+DEV uint32_t x_pair_f16(const typename XPair<XT>::T& v) {
     if constexpr (XT == XT_F16) {
-        return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
+        return v;
     } else if constexpr (XT == XT_BF16) {
-        const uint32_t b = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
-        return f2h(__builtin_bit_cast(float, b << 16)) | (f2h(__builtin_bit_cast(float, b & 0xffff0000u)) << 16);
+        return f2h(__builtin_bit_cast(float, v << 16)) | (f2h(__builtin_bit_cast(float, v & 0xffff0000u)) << 16);
     } else {
-        const float2 v = *reinterpret_cast<const float2*>(static_cast<const float*>(x) + i);
         return f2h(v.x) | (f2h(v.y) << 16);
     }
 }
 
+// Tile shapes.  A stage is BM weight rows x BK k (8192 weights: one
+// 32-element sub-block per thread of the 256).  BN = 16 (up to 16 tokens)
+// takes 64 rows x 128 k so a 14336-row weight spreads over 224 workgroups;
+// wider token tiles take 128 rows x 64 k.  PF stages of weights and
+// activations are in flight in registers, in the order they are consumed
+// (the memory counter retires loads in issue order).
+template <int BN> struct GemmTile;
+template <> struct GemmTile<16> { static constexpr int BM = 64, PF = 8; };
+template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
+template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 1; };
+
 template <typename D, int BN, int XT, int YT>
 __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
                           int m, int n, int k, int ldy) {
-    __shared__ __align__(16) uint16_t wl[2][GBM * GKP];
-    __shared__ __align__(16) uint16_t xl[2][BN * GKP];
+    constexpr int BM = GemmTile<BN>::BM, PF = GemmTile<BN>::PF;
+    constexpr int BK = 8192 / BM;       // k per stage
+    constexpr int KP = BK + 8;          // LDS row pitch in halves (pads away bank conflicts)
+    constexpr int SPR = BK / 32;        // sub-blocks per tile row and stage
+    constexpr int RA = BM / 64;         // 16-row MFMA tiles per wave
+    __shared__ __align__(16) uint16_t wl[2][BM * KP];
+    __shared__ __align__(16) uint16_t xl[2][BN * KP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * GBM, t0 = blockIdx.y * BN;
+    const int r0 = blockIdx.x * BM, t0 = blockIdx.y * BN;
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
-    const int nk = k / GBK;
+    const int nk = k / BK;
 
-    // weight: thread t dequantises sub-block 2*kb + (t & 1) of tile row t >> 1
-    const int wrow = tid >> 1, wsub = tid & 1;
-    const int grow = min(r0 + wrow, n - 1);
-    const uint8_t* wp = w + (size_t)grow * row_bytes;
-    // activations: BN x 64 halves per stage = BN * 32 pairs
-    constexpr int XPAIRS = BN * GBK / 2;
-    constexpr int XPT = (XPAIRS + 255) / 256;  // pairs per thread
-    typename D::Raw wr = D::load(wp, 2 * 0 + wsub);
-    uint32_t xr[XPT];
-    auto load_x = [&](int kb) {
+    // weights: thread t dequantises sub-block SPR*s + (t % SPR) of tile row t / SPR
+    const int wrow = tid / SPR, wsub = tid % SPR;
+    const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
+    // activations: BN x BK halves per stage, as f16 pairs
+    constexpr int XPAIRS = BN * BK / 2;
+    constexpr int XPT = (XPAIRS + 255) / 256;
+    struct Stage {
+        typename D::Raw wr;
+        typename XPair<XT>::T xr[XPT];
+    };
+    auto issue = [&](Stage& st, int s) {
+        const int sc = min(s, nk - 1);  // stages past the end re-load the last one
+        st.wr = D::load(wp, SPR * sc + wsub);
+        // never predicated (an index past the tile re-reads its last pair),
+        // so the loads retire in order without a drain
 #pragma unroll
         for (int p = 0; p < XPT; p++) {
-            const int pi = tid + 256 * p;
-            const int tok = pi / (GBK / 2), kk = 2 * (pi % (GBK / 2));
+            const int pi = min(tid + 256 * p, XPAIRS - 1);
+            const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
             const int gt = min(t0 + tok, m - 1);
-            xr[p] = (pi < XPAIRS) ? x_pair_f16<XT>(x, (size_t)gt * k + (size_t)kb * GBK + kk) : 0u;
+            st.xr[p] = x_pair_load<XT>(x, (size_t)gt * k + (size_t)sc * BK + kk);
         }
     };
-    load_x(0);
 
-    float4_t acc[2][BN / 16];
+    float4_t acc[RA][BN / 16];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < RA; a++)
 #pragma unroll
         for (int b = 0; b < BN / 16; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    for (int kb = 0; kb < nk; kb++) {
-        const int buf = kb & 1;
-        {   // dequantised weights -> LDS
-            uint32_t o[16];
-            D::deq(wr, 2 * kb + wsub, o);
-            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * GKP + 32 * wsub]);
+    Stage ring[PF];
 #pragma unroll
-            for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-        }
+    for (int i = 0; i < PF; i++) issue(ring[i], i);
+
+    for (int base = 0; base < nk; base += PF) {
 #pragma unroll
-        for (int p = 0; p < XPT; p++) {  // activations -> LDS (tokens past m are copies, never stored)
-            const int pi = tid + 256 * p;
-            if (pi < XPAIRS) {
-                const int tok = pi / (GBK / 2), kk = 2 * (pi % (GBK / 2));
-                *reinterpret_cast<uint32_t*>(&xl[buf][tok * GKP + kk]) = xr[p];
+        for (int b0 = 0; b0 < PF; b0++) {
+            const int s = base + b0;
+            if (s >= nk) break;
+            const int buf = s & 1;
+            Stage& st = ring[b0];
+            {   // dequantised weights -> LDS
+                uint32_t o[16];
+                D::deq(st.wr, SPR * s + wsub, o);
+                uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
             }
-        }
-        __syncthreads();
-        if (kb + 1 < nk) {
-            wr = D::load(wp, 2 * (kb + 1) + wsub);
-            load_x(kb + 1);
-        }
 #pragma unroll
-        for (int ks = 0; ks < GBK / 32; ks++) {
-            const int kof = 32 * ks + 8 * (lane >> 4);
-            half8_t av[2];
+            for (int p = 0; p < XPT; p++) {  // activations -> LDS (tokens past m are copies, never stored)
+                const int pi = tid + 256 * p;
+                if (pi < XPAIRS) {
+                    const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
+                    *reinterpret_cast<uint32_t*>(&xl[buf][tok * KP + kk]) = x_pair_f16<XT>(st.xr[p]);
+                }
+            }
+            __syncthreads();
+            issue(st, s + PF);
 #pragma unroll
-            for (int a = 0; a < 2; a++)
-                av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(32 * wave + 16 * a + (lane & 15)) * GKP + kof]);
+            for (int ks = 0; ks < BK / 32; ks++) {
+                const int kof = 32 * ks + 8 * (lane >> 4);
+                half8_t av[RA];
 #pragma unroll
-            for (int b = 0; b < BN / 16; b++) {
-                const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * GKP + kof]);
+                for (int a = 0; a < RA; a++)
+                    av[a] = *reinterpret_cast<const half8_t*>(
+                        &wl[buf][((BM / 4) * wave + 16 * a + (lane & 15)) * KP + kof]);
 #pragma unroll
-                for (int a = 0; a < 2; a++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
+                for (int b = 0; b < BN / 16; b++) {
+                    const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * KP + kof]);
+#pragma unroll
+                    for (int a = 0; a < RA; a++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
+                }
             }
         }
     }
 
     // lane holds D[4*(lane/16) + i][lane%16] of each 16x16 tile:
-    // weight row r0 + 32*wave + 16*a + 4*(lane/16) + i, token t0 + 16*b + lane%16
+    // weight row r0 + (BM/4)*wave + 16*a + 4*(lane/16) + i, token t0 + 16*b + lane%16
 #pragma unroll
-    for (int a = 0; a < 2; a++) {
+    for (int a = 0; a < RA; a++) {
 #pragma unroll
         for (int b = 0; b < BN / 16; b++) {
             const int tok = t0 + 16 * b + (lane & 15);
-            const int rb = r0 + 32 * wave + 16 * a + 4 * (lane >> 4);
+            const int rb = r0 + (BM / 4) * wave + 16 * a + 4 * (lane >> 4);
             if (tok < m) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
