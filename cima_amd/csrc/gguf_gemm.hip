@@ -265,11 +265,129 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
     }
 }
 
+// Wide token tiles (BN = 64, 128): v_mfma_f32_32x32x16_f16 on a 2 x 2 grid
+// of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
+// 128-row tile and tokens [wc BN/2, (wc+1) BN/2) -- so every A fragment
+// read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k
+// as in gemm_body; one (BN = 128) or two stages are in flight per
+// workgroup, and two workgroups share a CU.
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+template <typename D, int BN, int XT, int YT>
+__device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
+                               int m, int n, int k, int ldy) {
+    constexpr int BM = 128, BK = 64, KP = BK + 8, PF = BN == 64 ? 2 : 1;
+    constexpr int TB = BN / 64;  // 32-token MFMA tiles per wave
+    __shared__ __align__(16) uint16_t wl[2][BM * KP];
+    __shared__ __align__(16) uint16_t xl[2][BN * KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int r0 = blockIdx.x * BM, t0 = blockIdx.y * BN;
+    const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const int nk = k / BK;
+
+    const int wrow = tid >> 1, wsub = tid & 1;
+    const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
+    constexpr int XPAIRS = BN * BK / 2;
+    constexpr int XPT = XPAIRS / 256;
+    struct Stage {
+        typename D::Raw wr;
+        typename XPair<XT>::T xr[XPT];
+    };
+    auto issue = [&](Stage& st, int s) {
+        const int sc = min(s, nk - 1);
+        st.wr = D::load(wp, 2 * sc + wsub);
+#pragma unroll
+        for (int p = 0; p < XPT; p++) {
+            const int pi = tid + 256 * p;
+            const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
+            st.xr[p] = x_pair_load<XT>(x, (size_t)min(t0 + tok, m - 1) * k + (size_t)sc * BK + kk);
+        }
+    };
+
+    float16_t acc[2][TB];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < TB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
+
+    Stage ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) issue(ring[i], i);
+
+    for (int base = 0; base < nk; base += PF) {
+#pragma unroll
+        for (int b0 = 0; b0 < PF; b0++) {
+            const int s = base + b0;
+            if (s >= nk) break;
+            const int buf = s & 1;
+            Stage& st = ring[b0];
+            {
+                uint32_t o[16];
+                D::deq(st.wr, 2 * s + wsub, o);
+                uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+            }
+#pragma unroll
+            for (int p = 0; p < XPT; p++) {
+                const int pi = tid + 256 * p;
+                const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
+                *reinterpret_cast<uint32_t*>(&xl[buf][tok * KP + kk]) = x_pair_f16<XT>(st.xr[p]);
+            }
+            __syncthreads();
+            issue(st, s + PF);
+            // lane l: A[i = l%32][k = 8(l/32) + j], B[k = 8(l/32) + j][n = l%32]
+#pragma unroll
+            for (int ks = 0; ks < BK / 16; ks++) {
+                const int kof = 16 * ks + 8 * (lane >> 5);
+                half8_t av[2], bv[TB];
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+                    av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(64 * wr + 32 * a + (lane & 31)) * KP + kof]);
+#pragma unroll
+                for (int b = 0; b < TB; b++)
+                    bv[b] = *reinterpret_cast<const half8_t*>(
+                        &xl[buf][((BN / 2) * wc + 32 * b + (lane & 31)) * KP + kof]);
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+#pragma unroll
+                    for (int b = 0; b < TB; b++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
+            }
+        }
+    }
+
+    // lane l, element i of a 32x32 tile: row 8(i/4) + 4(l/32) + i%4, column l%32
+    // (weight row r0 + 64 wr + 32 a + row, token t0 + (BN/2) wc + 32 b + column)
+#pragma unroll
+    for (int a = 0; a < 2; a++) {
+#pragma unroll
+        for (int b = 0; b < TB; b++) {
+            const int tok = t0 + (BN / 2) * wc + 32 * b + (lane & 31);
+            if (tok >= m) continue;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = r0 + 64 * wr + 32 * a + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                if (row < n) {
+                    const size_t off = (size_t)tok * ldy + row;
+                    if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = acc[a][b][i];
+                    else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(acc[a][b][i]);
+                }
+            }
+        }
+    }
+}
+
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(256) void cima_gemm_##FN##_b##BN##_##XN##_##YN(          \
+    extern "C" __global__ __launch_bounds__(256, BN == 16 ? 1 : 2) void                             \
+    cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
-        gemm_body<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                           \
+        if constexpr (BN == 16) gemm_body<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                   \
+        else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
     }
 #define GEMM_XY(FN, D, BN)                                                    \
     GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F32, f32)                          \
