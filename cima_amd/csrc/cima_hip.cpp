@@ -509,6 +509,8 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
         return fail(CIMA_E_INVALID, "%s: shape m=%d n=%d k=%d: k must be a positive multiple of %d", api, m, n, k,
                     F->block_elems > 64 ? F->block_elems : 64);
     if (ldy < n) return fail(CIMA_E_INVALID, "%s: ldy=%d < n=%d", api, ldy, n);
+    if ((long long)m * k * (x_dtype == CIMA_DT_F32 ? 4 : 2) > 0xffffffffLL)
+        return fail(CIMA_E_INVALID, "%s: X of %d x %d is 4 GiB or more", api, m, k);
     if (x_dtype < CIMA_DT_F32 || x_dtype > CIMA_DT_BF16 || (y_dtype != CIMA_DT_F32 && y_dtype != CIMA_DT_F16))
         return fail(CIMA_E_INVALID, "%s: x_dtype %d / y_dtype %d not supported", api, x_dtype, y_dtype);
     if (m == 0 || n == 0) return 0;

@@ -25,6 +25,15 @@ DEV uint32_t f2h(float v) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+// two fp32 -> packed f16 bits (lo in bits 0-15) with one v_cvt_pk_f16_f32
+// (round to nearest even, like f2h); the empty asm has f2h's purpose
+DEV uint32_t f2h2(float lo, float hi) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    __asm__("" : "+v"(lo), "+v"(hi));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){lo, hi}, h2_t));
+}
+
 DEV uint4 ld16a(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 // 2-byte-aligned 16-byte load: gfx950 runs with unaligned global access
 // enabled, so this is one global_load_dwordx4 (measured at full streaming
@@ -71,8 +80,8 @@ struct FQ8_0 {
         for (int i = 0; i < 8; i++) {
             float v0 = d * (float)(int8_t)(w[i] & 0xff), v1 = d * (float)(int8_t)((w[i] >> 8) & 0xff);
             float v2 = d * (float)(int8_t)((w[i] >> 16) & 0xff), v3 = d * (float)(int8_t)(w[i] >> 24);
-            o[2 * i] = f2h(v0) | (f2h(v1) << 16);
-            o[2 * i + 1] = f2h(v2) | (f2h(v3) << 16);
+            o[2 * i] = f2h2(v0, v1);
+            o[2 * i + 1] = f2h2(v2, v3);
         }
         store32h(out, o);
     }
@@ -103,8 +112,8 @@ struct FQ4_0 {
                 int b0 = (q[i] >> (16 * j)) & 0xff, b1 = (q[i] >> (16 * j + 8)) & 0xff;
                 float l0 = d * (float)((b0 & 15) - 8), l1 = d * (float)((b1 & 15) - 8);
                 float h0 = d * (float)((b0 >> 4) - 8), h1 = d * (float)((b1 >> 4) - 8);
-                o[2 * i + j] = f2h(l0) | (f2h(l1) << 16);
-                o[8 + 2 * i + j] = f2h(h0) | (f2h(h1) << 16);
+                o[2 * i + j] = f2h2(l0, l1);
+                o[8 + 2 * i + j] = f2h2(h0, h1);
             }
         }
         store32h(out, o);
@@ -175,8 +184,8 @@ struct FQ4_K {
                 // fp32 rounding -- identical to the host decoder
                 float l0 = d0 * (float)(b0 & 15) - mm0, l1 = d0 * (float)(b1 & 15) - mm0;
                 float h0 = d1 * (float)(b0 >> 4) - mm1, h1 = d1 * (float)(b1 >> 4) - mm1;
-                ol[2 * i + j] = f2h(l0) | (f2h(l1) << 16);
-                oh[2 * i + j] = f2h(h0) | (f2h(h1) << 16);
+                ol[2 * i + j] = f2h2(l0, l1);
+                oh[2 * i + j] = f2h2(h0, h1);
             }
         }
         uint4* pl = reinterpret_cast<uint4*>(out);
@@ -249,8 +258,8 @@ struct FQ6_K {
                 float v1 = ds * (float)((int)((q[g][i] >> 8) & 0xff) - 32);
                 float v2 = ds * (float)((int)((q[g][i] >> 16) & 0xff) - 32);
                 float v3 = ds * (float)((int)((q[g][i] >> 24) & 0xff) - 32);
-                o[2 * i] = f2h(v0) | (f2h(v1) << 16);
-                o[2 * i + 1] = f2h(v2) | (f2h(v3) << 16);
+                o[2 * i] = f2h2(v0, v1);
+                o[2 * i + 1] = f2h2(v2, v3);
             }
             uint4* p = reinterpret_cast<uint4*>(out + 32 * g);
             p[0] = make_uint4(o[0], o[1], o[2], o[3]);

@@ -29,8 +29,8 @@ struct DQ8_0 {
         const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            o[2 * i] = f2h(d * (float)(int8_t)(w[i] & 0xff)) | (f2h(d * (float)(int8_t)((w[i] >> 8) & 0xff)) << 16);
-            o[2 * i + 1] = f2h(d * (float)(int8_t)((w[i] >> 16) & 0xff)) | (f2h(d * (float)(int8_t)(w[i] >> 24)) << 16);
+            o[2 * i] = f2h2(d * (float)(int8_t)(w[i] & 0xff), d * (float)(int8_t)((w[i] >> 8) & 0xff));
+            o[2 * i + 1] = f2h2(d * (float)(int8_t)((w[i] >> 16) & 0xff), d * (float)(int8_t)(w[i] >> 24));
         }
     }
 };
@@ -46,8 +46,8 @@ struct DQ4_0 {
 #pragma unroll
             for (int jj = 0; jj < 2; jj++) {
                 const int b0 = (q[i] >> (16 * jj)) & 0xff, b1 = (q[i] >> (16 * jj + 8)) & 0xff;
-                o[2 * i + jj] = f2h(d * (float)((b0 & 15) - 8)) | (f2h(d * (float)((b1 & 15) - 8)) << 16);
-                o[8 + 2 * i + jj] = f2h(d * (float)((b0 >> 4) - 8)) | (f2h(d * (float)((b1 >> 4) - 8)) << 16);
+                o[2 * i + jj] = f2h2(d * (float)((b0 & 15) - 8), d * (float)((b1 & 15) - 8));
+                o[8 + 2 * i + jj] = f2h2(d * (float)((b0 >> 4) - 8), d * (float)((b1 >> 4) - 8));
             }
         }
     }
@@ -76,9 +76,10 @@ struct DQ4_K {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t n = hi ? ((q[i] >> 4) & 0x0F0F0F0Fu) : (q[i] & 0x0F0F0F0Fu);
-            // (d*sc)*q is exact, so the subtraction is the only fp32 rounding
-            o[2 * i] = f2h(ds * (float)(n & 0xff) - mm) | (f2h(ds * (float)((n >> 8) & 0xff) - mm) << 16);
-            o[2 * i + 1] = f2h(ds * (float)((n >> 16) & 0xff) - mm) | (f2h(ds * (float)(n >> 24) - mm) << 16);
+            // (d*sc)*q is exact, so the subtraction is the only fp32
+            // rounding -- and a fused multiply-add rounds exactly there too
+            o[2 * i] = f2h2(__builtin_fmaf(ds, (float)(n & 0xff), -mm), __builtin_fmaf(ds, (float)((n >> 8) & 0xff), -mm));
+            o[2 * i + 1] = f2h2(__builtin_fmaf(ds, (float)((n >> 16) & 0xff), -mm), __builtin_fmaf(ds, (float)(n >> 24), -mm));
         }
     }
 };
@@ -111,8 +112,8 @@ struct DQ6_K {
         for (int i = 0; i < 8; i++) {
             const float ds = i < 4 ? ds0 : ds1;
             const uint32_t q = ((a[i] >> nsh) & 0x0F0F0F0Fu) | (((h[i] >> hsh) & 0x03030303u) << 4);
-            o[2 * i] = f2h(ds * (float)((int)(q & 0xff) - 32)) | (f2h(ds * (float)((int)((q >> 8) & 0xff) - 32)) << 16);
-            o[2 * i + 1] = f2h(ds * (float)((int)((q >> 16) & 0xff) - 32)) | (f2h(ds * (float)((int)(q >> 24) - 32)) << 16);
+            o[2 * i] = f2h2(ds * (float)((int)(q & 0xff) - 32), ds * (float)((int)((q >> 8) & 0xff) - 32));
+            o[2 * i + 1] = f2h2(ds * (float)((int)((q >> 16) & 0xff) - 32), ds * (float)((int)(q >> 24) - 32));
         }
     }
 };
@@ -123,10 +124,14 @@ struct DQ6_K {
 template <int XT> struct XPair { using T = uint32_t; };
 template <> struct XPair<XT_F32> { using T = float2; };
 
+// pair at element offset i: a 32-bit byte offset from the uniform base, so
+// the load takes the base in scalar registers and one vector offset (the
+// host keeps X under 4 GiB)
 template <int XT>
-DEV typename XPair<XT>::T x_pair_load(const void* x, size_t i) {
-    if constexpr (XT == XT_F32) return *reinterpret_cast<const float2*>(static_cast<const float*>(x) + i);
-    else return *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + i);
+DEV typename XPair<XT>::T x_pair_load(const void* x, uint32_t i) {
+    const uint8_t* b = static_cast<const uint8_t*>(x);
+    if constexpr (XT == XT_F32) return *reinterpret_cast<const float2*>(b + i * 4u);
+    else return *reinterpret_cast<const uint32_t*>(b + i * 2u);
 }
 
 template <int XT>
@@ -134,9 +139,9 @@ DEV uint32_t x_pair_f16(const typename XPair<XT>::T& v) {
     if constexpr (XT == XT_F16) {
         return v;
     } else if constexpr (XT == XT_BF16) {
-        return f2h(__builtin_bit_cast(float, v << 16)) | (f2h(__builtin_bit_cast(float, v & 0xffff0000u)) << 16);
+        return f2h2(__builtin_bit_cast(float, v << 16), __builtin_bit_cast(float, v & 0xffff0000u));
     } else {
-        return f2h(v.x) | (f2h(v.y) << 16);
+        return f2h2(v.x, v.y);
     }
 }
 
@@ -186,7 +191,7 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
             const int pi = min(tid + 256 * p, XPAIRS - 1);
             const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
             const int gt = min(t0 + tok, m - 1);
-            st.xr[p] = x_pair_load<XT>(x, (size_t)gt * k + (size_t)sc * BK + kk);
+            st.xr[p] = x_pair_load<XT>(x, (uint32_t)(gt * k + sc * BK + kk));
         }
     };
 
@@ -301,7 +306,7 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
         for (int p = 0; p < XPT; p++) {
             const int pi = tid + 256 * p;
             const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
-            st.xr[p] = x_pair_load<XT>(x, (size_t)min(t0 + tok, m - 1) * k + (size_t)sc * BK + kk);
+            st.xr[p] = x_pair_load<XT>(x, (uint32_t)(min(t0 + tok, m - 1) * k + sc * BK + kk));
         }
     };
 
