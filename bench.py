@@ -14,10 +14,13 @@ Weights are seeded synthetic N(0, 0.02) quantised to Q4_K; x ~ N(0, 1).
 
 value = algorithmic bytes per step (packed weights + fp32 x and y) x steps /
 time, in GB/s.  Per-shape us/call (cold, graph-batched) for configs 1-3 are
-reported under "shapes"; "roofline" is for the fused gate+up kernel, the
+reported under "shapes" (with the plain streaming-read time of the same
+weight bytes, the best any kernel reads them here, and Q8_0 at the same
+Llama-3-8B shapes); "roofline" is for the fused gate+up kernel, the
 largest share of a step, timed with HIP events on its launch stream;
 "cpu_baseline" runs the CPU restatement of the reference's host path
-(decode to f16, fp32 dot) on a bounded sample of the same step.
+(decode to f16, fp32 dot) on a bounded sample of the same step, single
+threaded like the reference's loops and again on all host cores.
 
 Usage: python bench.py [--gpus 1] [--steps 320] [--warmup 64]
 """
@@ -169,6 +172,7 @@ def main():
         return best
 
     per_shape = {}
+    read_us = {}
     gemm_flops = {}
     # the roofline kernel: fused gate+up SwiGLU, cold over the 32 layers
     pair_bytes = 2 * wbytes(Q4_K, FFN, HID) + 4 * HID + 4 * FFN
@@ -182,7 +186,7 @@ def main():
     for b in rbufs:
         b.fill_(1)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    read_us = time_calls(lambda b: ctx.stream_read(b, rbytes, sink), rbufs)
+    pair_read_us = time_calls(lambda b: ctx.stream_read(b, rbytes, sink), rbufs)
     del rbufs
     if not args.no_shapes:
         def shape_leg(name, t, n, k, copies_mb=600):
@@ -191,14 +195,21 @@ def main():
             bufs = [torch.from_numpy(w).to(dev) for _ in range(ncopy)]
             xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev)
             ys = torch.empty(n, device=dev)
-            us = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs,
-                            calls=max(16, min(64, 2 * ncopy)))
+            calls = max(16, min(64, 2 * ncopy))
+            us = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs, calls=calls)
             per_shape[name] = (us, wbytes(t, n, k) + 4 * (n + k))
+            # the streaming-read time of the same weight bytes, same method
+            rb = w.nbytes // 16 * 16
+            read_us[name] = time_calls(lambda b: ctx.stream_read(b, rb, sink), bufs, calls=calls)
             return us
         for nm, (n, k) in [("q4_k 6144x4096 (q|k|v)", (HID + 2 * KV, HID)),
                            ("q4_k 14336x4096 (gate/up)", (FFN, HID)), ("q4_k 4096x14336 (down)", (HID, FFN)),
                            ("q4_k 4096x4096 (q/o)", (HID, HID)), ("q4_k 1024x4096 (k/v)", (KV, HID))]:
             shape_leg(nm, Q4_K, n, k)
+        # Q8_0 at the same Llama-3-8B layer shapes
+        for nm, (n, k) in [("q8_0 14336x4096 (gate/up)", (FFN, HID)), ("q8_0 4096x14336 (down)", (HID, FFN)),
+                           ("q8_0 4096x4096 (q/o)", (HID, HID))]:
+            shape_leg(nm, Q8_0, n, k)
         shape_leg("q8_0 4864x896 (config 1)", Q8_0, 4864, 896)
         shape_leg("q6_k 128256x4096 (config 3 head)", Q6_K, 128256, HID, copies_mb=900)
         # config 4: prefill dequant-GEMM on MFMA, Q4_K 14336x4096, X bf16 (m tokens), Y fp32
@@ -216,6 +227,9 @@ def main():
     for name, (us, b) in per_shape.items():
         shapes_out[name] = {"us_per_call": round(us, 3), "gb_s": round(b / us / 1e3, 1),
                             "hbm_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": b}
+        if name in read_us:
+            shapes_out[name]["read_ceiling_us"] = round(read_us[name], 3)
+            shapes_out[name]["frac_of_read_ceiling"] = round(read_us[name] / us, 4)
         if name in gemm_flops:
             tf = gemm_flops[name] / us / 1e6
             shapes_out[name].update({"tflop_s": round(tf, 1), "mfma_frac_f16_dense": round(tf / 2500.0, 4)})
@@ -231,8 +245,8 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "kernel": "cima_gemv_q4_k_r1_i1_f32_pair", "alg_bytes_per_launch": pair_bytes,
                 "avg_launch_us": round(pair_us, 3),
-                "read_ceiling_gb_s": round(rbytes / read_us / 1e3, 1),
-                "frac_of_read_ceiling": round(achieved / (rbytes / read_us / 1e3), 4)}
+                "read_ceiling_gb_s": round(rbytes / pair_read_us / 1e3, 1),
+                "frac_of_read_ceiling": round(achieved / (rbytes / pair_read_us / 1e3), 4)}
 
     # ---- config 5: whole greedy decode step of a Qwen2.5-0.5B-shaped Q8_0
     # model, KV prefilled to 2048, one graph replay per token
@@ -295,11 +309,24 @@ def main():
                 n, k = shapes[name]
                 oracle.gguf_gemv_packed(Q4_K, host[name], xin, n, k, threads=1)
         cpu_s = time.perf_counter() - t0
+        # the same sample on every host core this process may use (at most
+        # 16, the box's CPU share per GPU), rows split over OpenMP threads
+        ncores = min(16, len(os.sched_getaffinity(0)))
+        t0 = time.perf_counter()
+        for _ in range(args.cpu_steps):
+            for name, xin in order:
+                n, k = shapes[name]
+                oracle.gguf_gemv_packed(Q4_K, host[name], xin, n, k, threads=ncores)
+        mt_s = time.perf_counter() - t0
         cpu = {"value": round(step_bytes * args.cpu_steps / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                "kind": "port",
                "sample": f"{args.cpu_steps} layer steps (same 7 Q4_K GEMVs, same weights), single thread, "
                          f"{cpu_s:.1f} s; oracle/gguf_oracle.c decode-to-f16 + fp32 dot",
-               "ms_per_step": round(cpu_s * 1e3 / args.cpu_steps, 1)}
+               "ms_per_step": round(cpu_s * 1e3 / args.cpu_steps, 1),
+               "all_cores": {"value": round(step_bytes * args.cpu_steps / mt_s / 1e9, 4), "unit": "GB/s",
+                             "cores": ncores, "ms_per_step": round(mt_s * 1e3 / args.cpu_steps, 1),
+                             "sample": f"the same {args.cpu_steps} layer steps, rows over {ncores} threads, "
+                                       f"{mt_s:.1f} s"}}
 
     out = {
         "metric": "dequant-GEMV µs/call + % HBM roofline (Q4_K/Q8_0, 8B shapes); decode tok/s",

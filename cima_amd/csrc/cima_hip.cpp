@@ -201,11 +201,11 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     long groups_per_wg = (long)(kGemvThreads / 64) * (64 / lpr);
     long row_groups = ((long)n + rows - 1) / rows;
     long wgs = (row_groups + groups_per_wg - 1) / groups_per_wg;
-    // the item-ring loop for large matrices of one-unit rows (measured
+    // the item-ring loop for large matrices of one- or two-unit rows (measured
     // faster from about 8 MB of weights up; smaller ones are latency-bound
     // and finish sooner with the plain double buffer)
     const double wbytes = (double)n * (double)(k / F->block_elems) * F->block_bytes;
-    const bool ring = !pair && rows == 1 && it == 1 && (ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6));
+    const bool ring = !pair && rows == 1 && it <= 2 && (ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6));
     return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring};
 }
 
@@ -335,11 +335,12 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
                     if (!rc) rc = add(0, name);
                 }
-        for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"}) {
-            char name[96];
-            snprintf(name, sizeof name, "cima_gemv_%s_r1_i1%s", F->name, rk);
-            if (!rc) rc = add(0, name);
-        }
+        for (int it = 1; it <= 2; it++)
+            for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"}) {
+                char name[96];
+                snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
+                if (!rc) rc = add(0, name);
+            }
         for (int bn : kGemmBN)
             for (const char* xt : {"f32", "f16", "bf16"})
                 for (const char* yt : {"f32", "f16"}) {
@@ -859,7 +860,7 @@ int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, u
     long long n16 = nbytes / 16;
     if (n16 == 0) return 0;
     long long grid = (n16 + 4 * 256 - 1) / (4 * 256);
-    if (grid > 4L * ctx->num_cu) grid = 4L * ctx->num_cu;
+    if (grid > 2L * ctx->num_cu) grid = 2L * ctx->num_cu;
     void* args[] = {&src, &n16, &sink};
     return launch_named(ctx, "cima_stream_read", (unsigned)grid, 256, args, api);
 }

@@ -209,6 +209,15 @@ struct IQ6_K {
 constexpr int GNW = 4;
 constexpr int GNT = 64 * GNW;
 
+// Item-ring depth: row groups in flight per lane for items of one unit of
+// one weight stream, and for items of two (two units, or the gate|up pair)
+#ifndef CIMA_RING_DEPTH
+#define CIMA_RING_DEPTH 4
+#endif
+#ifndef CIMA_RING_DEPTH_PAIR
+#define CIMA_RING_DEPTH_PAIR 2
+#endif
+
 // sum over the workgroup (every thread calls it; all get the total)
 DEV float block_sum(float v) {
     __shared__ float red[GNW];
@@ -258,36 +267,26 @@ DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
 // Optional RMSNorm prologue (k_rmsnorm, src/kernels.cu:37-50): with norm_w
 // set, the GEMV multiplies W by h = f16(sat(x) * rsqrt(mean(sat(x)^2) + eps)
 // * norm_w) instead of x -- h is rounded to f16 (f32 activations: kept in
-// fp32) as the reference's separate rmsnorm launch writes it.
-template <int ACT>
-DEV float norm_scale(const void* __restrict__ x, int k, float eps) {
-    float ss = 0.f;
-    for (int c = threadIdx.x; c < (k >> 4); c += GNT) {
-        float v[16];
-        load16<ACT>(x, c, v);
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float s = sat16(v[i]);
-            ss += s * s;
-        }
-    }
-    return 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
-}
+// fp32) as the reference's separate rmsnorm launch writes it (stage_x).
+#ifdef CIMA_PROBE_TIMES
+// per-workgroup timestamps of an instrumented build (never in the product)
+__device__ unsigned long long g_probe_ts[8192 * 16];
+#endif
 
-// x staging.  Thread t owns 16-element chunks base + t + GNT j (j < XB) of
-// every batch; a batch's raw loads are issued together -- for the first
-// batch before the GEMV's first weight row, so x and weights arrive in one
-// round trip -- and held in registers through the RMSNorm reduction.  XB is
+// x staging.  Thread t owns 16-element chunks t + GNT j (j < XB); their raw
+// loads are issued together before the GEMV's first weight rows, so x and
+// weights arrive in one round trip, and held in registers through the
+// RMSNorm reduction.  XB is
 // sized to the row length the kernel variant is built for (ITERS units of
-// every one of up to 64 lanes), so one batch covers x in the common case.
+// every one of up to 64 lanes), so one batch covers x.
 template <int ACT, int XB>
 struct XBatch {
     static constexpr int U = ACT == ACT_F32 ? 4 : 2;  // uint4 per chunk
     uint4 u[XB][U];
-    DEV void load(const void* __restrict__ x, int base, int nck) {
+    DEV void load(const void* __restrict__ x, int nck) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
-            const int c = min(base + (int)threadIdx.x + GNT * j, nck - 1);
+            const int c = min((int)threadIdx.x + GNT * j, nck - 1);
             const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + (size_t)c * 16 * U);
 #pragma unroll
             for (int i = 0; i < U; i++) u[j][i] = p[i];
@@ -322,22 +321,32 @@ DEV void quant_chunk(const float v[16], int c, bool ok, uint8_t* xq, float* xs, 
     amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, amax), 0xB1, 0xf, 0xf, false)));
     const float qinv = amax > 0.f ? 32639.f / amax : 0.f;
     const float scale = amax * (1.0f / 32639.f);
+    // q = rint(v * qinv) by the float rounding of t + 1.5 * 2^23 (|t| <
+    // 2^15, so the sum rounds to an integer, to nearest even, exactly as
+    // rintf(t)); the extra +128 makes the two low bytes of the sum's bits
+    // those of q' = q + 128.  With q = 256 hi + lo, lo in [-128, 127]:
+    // lo = byte0(q') ^ 0x80 and hi = byte1(q') (two's complement).
+    constexpr float kMagic = 12582912.0f + 128.0f;
+    constexpr uint32_t kMagicBits = 0x4B400080u;
+    uint32_t b[16];
+    uint32_t bsum = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float t = v[i] * qinv;
+        b[i] = __builtin_bit_cast(uint32_t, t + kMagic);
+        bsum += b[i];
+    }
+    const int qsum = (int)(bsum - 16u * kMagicBits);
     uint32_t hw[4], lw[4];
-    int qsum = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        uint32_t hv = 0, lv = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int q = (int)__builtin_rintf(v[4 * i + j] * qinv);
-            const int hi = (q + 128) >> 8;
-            const int lo = q - (hi << 8);
-            hv |= (uint32_t)(hi & 0xff) << (8 * j);
-            lv |= (uint32_t)(lo & 0xff) << (8 * j);
-            qsum += q;
-        }
-        hw[i] = hv;
-        lw[i] = lv;
+        // byte 1 of b[4i..4i+3] -> hw[i]; byte 0 -> lw[i]
+        const uint32_t h01 = __builtin_amdgcn_perm(b[4 * i + 1], b[4 * i], 0x0c0c0501u);
+        const uint32_t h23 = __builtin_amdgcn_perm(b[4 * i + 3], b[4 * i + 2], 0x05010c0cu);
+        const uint32_t l01 = __builtin_amdgcn_perm(b[4 * i + 1], b[4 * i], 0x0c0c0400u);
+        const uint32_t l23 = __builtin_amdgcn_perm(b[4 * i + 3], b[4 * i + 2], 0x04000c0cu);
+        hw[i] = h01 | h23;
+        lw[i] = (l01 | l23) ^ 0x80808080u;
     }
     if (ok) {
         uint4* dst = reinterpret_cast<uint4*>(xq + chunk_off<PADSH>(c));
@@ -350,62 +359,66 @@ DEV void quant_chunk(const float v[16], int c, bool ok, uint8_t* xq, float* xs, 
     }
 }
 
-// x -> LDS from the first batch already in flight in `xb` (later batches,
-// k > 256 * XB * 16, are loaded here).  With norm_w, x is first replaced by
-// its RMSNorm (sum of squares from the registers when x fits one batch).
+// x -> LDS from the batch already in flight in `xb`, which covers the
+// whole row: the variant serves rows of at most 64 lanes x ITERS units, and
+// XB is sized for that, so staging is one straight pass (no loop-carried
+// registers, which would make the compiler copy the weight registers still
+// in flight and wait for them).  With norm_w, x is first replaced by its
+// RMSNorm (sum of squares from the registers).
 template <int ACT, int XB, int PADSH>
 DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t* xq, float* xs, float* xsum,
                  const void* __restrict__ norm_w, float eps) {
-    const int nck = k >> 4;
+    const int nck = k >> 4;  // <= GNT * XB
     const int t = threadIdx.x;
     float inv = 1.f;
     if (norm_w) {
-        if (nck <= GNT * XB) {
-            float ss = 0.f;
-#pragma unroll
-            for (int j = 0; j < XB; j++) {
-                float v[16];
-                xb.get(j, v);
-                float sj = 0.f;
-#pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float sv = sat16(v[i]);
-                    sj += sv * sv;
-                }
-                ss += t + GNT * j < nck ? sj : 0.f;
-            }
-            inv = 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
-        } else {
-            inv = norm_scale<ACT>(x, k, eps);
-        }
-    }
-    for (int base = 0; base < nck; base += GNT * XB) {
-        if (base) xb.load(x, base, nck);
+        float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < XB; j++) {
-            const int c = base + t + GNT * j;
             float v[16];
             xb.get(j, v);
-            if (norm_w) {
-                float g[16];
-                load16<ACT>(norm_w, min(c, nck - 1), g);
+            float sj = 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const float h = sat16(v[i]) * inv * g[i];
-                    if constexpr (ACT == ACT_F32) v[i] = h;
-                    else v[i] = h2f(f2h(h));
-                }
+            for (int i = 0; i < 16; i++) {
+                const float sv = sat16(v[i]);
+                sj += sv * sv;
             }
-            quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
+            ss += t + GNT * j < nck ? sj : 0.f;
         }
+        inv = 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
     }
+#ifdef CIMA_PROBE_TIMES
+    {
+        uint32_t z = 0;
+#pragma unroll
+        for (int j = 0; j < XB; j++) z ^= xb.u[j][0].x ^ xb.u[j][XBatch<ACT, XB>::U - 1].w;
+        if (z == 0x9E3779B9u) xs[0] = 0.f;
+        if ((threadIdx.x & 63) == 0) g_probe_ts[blockIdx.x * 16 + 10 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime();
+    }
+#endif
+#pragma unroll
+    for (int j = 0; j < XB; j++) {
+        const int c = t + GNT * j;
+        float v[16];
+        xb.get(j, v);
+        if (norm_w) {
+            float g[16];
+            load16<ACT>(norm_w, min(c, nck - 1), g);
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float h = sat16(v[i]) * inv * g[i];
+                if constexpr (ACT == ACT_F32) v[i] = h;
+                else v[i] = h2f(f2h(h));
+            }
+        }
+        quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
+    }
+#ifdef CIMA_PROBE_TIMES
+    if ((threadIdx.x & 63) == 0) g_probe_ts[blockIdx.x * 16 + 6 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime();
+#endif
     __syncthreads();
 }
 
-#ifdef CIMA_PROBE_TIMES
-// per-workgroup timestamps of an instrumented build (never in the product)
-__device__ unsigned long long g_probe_ts[8192 * 16];
-#endif
 
 // Optional operands of the fused prologues and epilogues, passed by value.
 struct GemvExt {
@@ -569,7 +582,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             float* xt = reinterpret_cast<float*>(lds + ((xstage_bytes<F::PADSH>(k) + 15) & ~15));
             stage_attn(static_cast<const float*>(x), k, ext, xt);
             XBatch<ACT_F32, XB> xa;
-            xa.load(xt, 0, k >> 4);
+            xa.load(xt, k >> 4);
             stage_x<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
         } else {
             stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
@@ -641,15 +654,15 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     };
 
     if constexpr (RING) {
-        // Item ring (single-row, one-unit-per-lane rows): item q is the
-        // lane's q-th row group; DEPTH items are in flight in a ring of
-        // slots and the loop body is unrolled over DEPTH items so slot
+        // Item ring (single-row rows of one or two units per lane): item q
+        // is the lane's q-th row group; DEPTH items are in flight in a ring
+        // of slots and the loop body is unrolled over DEPTH items so slot
         // indices are compile-time constants.  Items past the lane's last
         // row group re-load that row group (a cache hit) and write nothing.
-        static_assert(ITERS == 1, "the item ring serves one-unit rows");
-        constexpr int DEPTH = S >= 2 ? 2 : 4;
+        static_assert(ITERS <= 2 && R == 1, "the item ring serves one-row groups of one or two units");
+        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
         struct Item {
-            typename F::Raw w[S];
+            typename F::Raw w[S][ITERS];
             float e1[R], e2[R];
         };
         auto issue = [&](Item& dst, int q) {
@@ -657,23 +670,31 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int row = min(g * R + (s % R), n - 1);
-                dst.w[s] = F::load(((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes, uu[0]);
+                const uint8_t* rp = ((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes;
+#pragma unroll
+                for (int j = 0; j < ITERS; j++) dst.w[s][j] = F::load(rp, uu[j]);
             }
             if constexpr (EPI) epi_load(dst.e1, dst.e2, g);
         };
         Item ring[DEPTH];
         XBatch<ACT, XB> xb;
-        if constexpr (XS == 0) xb.load(x, 0, k >> 4);
+        if constexpr (XS == 0) xb.load(x, k >> 4);
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
         stage(xb);
-        F::loadx(xq, xs, xsum, uu[0], xreg);
+        typename F::Xf xr[ITERS];
+#pragma unroll
+        for (int j = 0; j < ITERS; j++) F::loadx(xq, xs, xsum, uu[j], xr[j]);
         for (int base = 0; base < per; base += DEPTH) {
 #pragma unroll
             for (int b = 0; b < DEPTH; b++) {
                 float acc[S];
 #pragma unroll
-                for (int s = 0; s < S; s++) acc[s] = uok[0] ? wdot(ring[b].w[s], xreg, uu[0]) : 0.f;
+                for (int s = 0; s < S; s++) {
+                    acc[s] = 0.f;
+#pragma unroll
+                    for (int j = 0; j < ITERS; j++) acc[s] += uok[j] ? wdot(ring[b].w[s][j], xr[j], uu[j]) : 0.f;
+                }
                 finish(acc, ring[b].e1, ring[b].e2, base + b);
                 issue(ring[b], base + b + DEPTH);
             }
@@ -719,7 +740,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         };
         Slot bufA, bufB;
         XBatch<ACT, XB> xb;
-        if constexpr (XS == 0) xb.load(x, 0, k >> 4);
+        if constexpr (XS == 0) xb.load(x, k >> 4);
         issue(bufA, 0);
         stage(xb);
         if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
@@ -776,14 +797,15 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #define GEMV_ACT(FN, F, R, IT) GEMV_EPI(FN, F, R, IT, ACT_F32, f32) GEMV_EPI(FN, F, R, IT, ACT_F16, f16) \
     GEMV_DECODE(FN, F, R, IT)
 
-// item-ring variants (one row, one unit per lane; tall matrices):
-// cima_gemv_<fmt>_r1_i1_<f32|f16>_ring[_epi], cima_gemv_<fmt>_r1_i1_f16_ring_amax
-#define GEMV_RING(FN, F)                                                                              \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f32_ring, F, 1, 1, ACT_F32, 0, 0, 0, 0, 1)                       \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f32_ring_epi, F, 1, 1, ACT_F32, 0, 1, 0, 0, 1)                   \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring, F, 1, 1, ACT_F16, 0, 0, 0, 0, 1)                       \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring_epi, F, 1, 1, ACT_F16, 0, 1, 0, 0, 1)                   \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i1_f16_ring_amax, F, 1, 1, ACT_F16, 0, 0, 0, 1, 1)
+// item-ring variants (one row, one or two units per lane; large matrices):
+// cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ring[_epi], cima_gemv_<fmt>_r1_i<1|2>_f16_ring_amax
+#define GEMV_RING_IT(FN, F, IT)                                                                        \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring, F, 1, IT, ACT_F32, 0, 0, 0, 0, 1)                  \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring_epi, F, 1, IT, ACT_F32, 0, 1, 0, 0, 1)              \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring, F, 1, IT, ACT_F16, 0, 0, 0, 0, 1)                  \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 1)              \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_amax, F, 1, IT, ACT_F16, 0, 0, 0, 1, 1)
+#define GEMV_RING(FN, F) GEMV_RING_IT(FN, F, 1) GEMV_RING_IT(FN, F, 2)
 
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \

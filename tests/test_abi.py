@@ -50,8 +50,9 @@ def test_code_object_holds_every_kernel():
             for a in ("f32", "f16"):
                 for sfx in ("", "_epi", "_pair", "_pair_epi") + (("_att_epi", "_amax") if a == "f16" else ()):
                     assert f"cima_gemv_{f}_r{r}_i{it}_{a}{sfx}".encode() in blob
-        for rk in ("_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"):
-            assert f"cima_gemv_{f}_r1_i1{rk}".encode() in blob
+        for it in (1, 2):
+            for rk in ("_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"):
+                assert f"cima_gemv_{f}_r1_i{it}{rk}".encode() in blob
         assert f"cima_dequant_{f}".encode() in blobs["dequant"]
         assert f"cima_gather_{f}".encode() in blobs["dequant"]
         for bn in (16, 64, 128):

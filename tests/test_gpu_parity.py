@@ -385,7 +385,8 @@ def test_launches_order_with_torch_default_stream(hip):
 def test_item_ring_matches_double_buffer(t):
     """The item-ring main loop (forced on with CIMA_GEMV_RING=1, forced off
     with 2) computes every row exactly as the row-group double buffer does:
-    identical outputs, f32 and f16, with and without the epilogue."""
+    identical outputs, f32 and f16, with and without the epilogue, for rows
+    of one and of two units per lane (ragged included)."""
     import os
     from cima_amd.hip import HipCtx
 
@@ -398,8 +399,9 @@ def test_item_ring_matches_double_buffer(t):
             del os.environ["CIMA_GEMV_RING"]
         ctxs[mode].use_torch_stream()
     be = {2: 32, 8: 32, 12: 256, 14: 256}[t]
-    k = 64 * (64 if be == 256 else 32) // 2  # one unit per lane at 32 lanes
-    for n in (1, 37, 1000):
+    ue = 64 if be == 256 else 32  # elements per unit
+    # one unit per lane at 32 lanes; two per lane at 64 (ragged: 100 units)
+    for n, k in ((1, 32 * ue), (37, 32 * ue), (1000, 32 * ue), (37, 128 * ue), (300, 100 * ue)):
         w = torch.from_numpy(synth.weights(t, 80 + n, 0.02, n, k)).cuda()
         for dt in (torch.float32, torch.float16):
             x = torch.from_numpy(synth.normal(81, 1.0, k)).to(dt).cuda()
@@ -412,6 +414,6 @@ def test_item_ring_matches_double_buffer(t):
                 c.gguf_gemv(t, x, w, None, y0, n, k, 0)
                 outs.append((y, y0))
             torch.cuda.synchronize()
-            assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (n, dt)
+            assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (n, k, dt)
     for c in ctxs.values():
         c.close()
