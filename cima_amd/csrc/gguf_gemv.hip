@@ -282,8 +282,13 @@ __device__ unsigned long long g_probe_ts[8192 * 16];
 template <int ACT, int XB>
 struct XBatch {
     static constexpr int U = ACT == ACT_F32 ? 4 : 2;  // uint4 per chunk
+    // f16 rows of up to 2 x 4096 elements also hold the RMSNorm weights, so
+    // they too are loaded ahead of the weight rows (longer or f32 rows load
+    // them while staging, after the weight rows are issued)
+    static constexpr bool G = ACT == ACT_F16 && XB <= 2;
     uint4 u[XB][U];
-    DEV void load(const void* __restrict__ x, int nck) {
+    uint4 g[G ? XB : 1][U];
+    DEV void load(const void* __restrict__ x, int nck, const void* __restrict__ nw = nullptr) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
             const int c = min((int)threadIdx.x + GNT * j, nck - 1);
@@ -291,19 +296,41 @@ struct XBatch {
 #pragma unroll
             for (int i = 0; i < U; i++) u[j][i] = p[i];
         }
+        if constexpr (G) {
+            if (nw) {
+#pragma unroll
+                for (int j = 0; j < XB; j++) {
+                    const int c = min((int)threadIdx.x + GNT * j, nck - 1);
+                    const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(nw) + (size_t)c * 16 * U);
+#pragma unroll
+                    for (int i = 0; i < U; i++) g[j][i] = p[i];
+                }
+            }
+        }
+    }
+    // norm weights of chunk j (c = threadIdx.x + GNT j)
+    DEV void get_norm(const void* __restrict__ nw, int j, int c, float v[16]) const {
+        if constexpr (G) {
+#pragma unroll
+            for (int i = 0; i < U; i++) unpack(g[j][i], v + 8 * i);
+        } else {
+            load16<ACT>(nw, c, v);
+        }
     }
     DEV void get(int j, float v[16]) const {
 #pragma unroll
-        for (int i = 0; i < U; i++) {
-            const uint32_t w[4] = {u[j][i].x, u[j][i].y, u[j][i].z, u[j][i].w};
+        for (int i = 0; i < U; i++) unpack(u[j][i], v + (16 / U) * i);
+    }
+    // one uint4 -> 4 fp32 or 8 f16 values
+    DEV static void unpack(uint4 q, float* v) {
+        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if constexpr (ACT == ACT_F32) {
-                    v[4 * i + e] = __builtin_bit_cast(float, w[e]);
-                } else {
-                    v[8 * i + 2 * e] = h2f(w[e] & 0xffffu);
-                    v[8 * i + 2 * e + 1] = h2f(w[e] >> 16);
-                }
+        for (int e = 0; e < 4; e++) {
+            if constexpr (ACT == ACT_F32) {
+                v[e] = __builtin_bit_cast(float, w[e]);
+            } else {
+                v[2 * e] = h2f(w[e] & 0xffffu);
+                v[2 * e + 1] = h2f(w[e] >> 16);
             }
         }
     }
@@ -403,7 +430,7 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
         xb.get(j, v);
         if (norm_w) {
             float g[16];
-            load16<ACT>(norm_w, min(c, nck - 1), g);
+            xb.get_norm(norm_w, j, min(c, nck - 1), g);
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const float h = sat16(v[i]) * inv * g[i];
@@ -678,7 +705,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         };
         Item ring[DEPTH];
         XBatch<ACT, XB> xb;
-        if constexpr (XS == 0) xb.load(x, k >> 4);
+        if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
         stage(xb);
@@ -740,7 +767,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         };
         Slot bufA, bufB;
         XBatch<ACT, XB> xb;
-        if constexpr (XS == 0) xb.load(x, k >> 4);
+        if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
         issue(bufA, 0);
         stage(xb);
         if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);

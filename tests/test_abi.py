@@ -161,3 +161,41 @@ def test_synth_rejects_bad_shapes():
         synth.quantize(12, np.zeros((2, 100), np.float32))
     with pytest.raises(ValueError):
         synth.weights(13, 1, 0.02, 2, 256)
+
+
+def _kernel_notes(hsaco):
+    """(vgpr_count, private_segment_fixed_size) per kernel of a built code
+    object, read from its AMDGPU metadata with the ROCm LLVM tools."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    llvm = "/opt/rocm/llvm/bin"
+    if not (shutil.which(f"{llvm}/clang-offload-bundler") and shutil.which(f"{llvm}/llvm-readelf")):
+        pytest.skip("ROCm LLVM tools not found")
+    with tempfile.TemporaryDirectory() as d:
+        co = os.path.join(d, "k.co")
+        subprocess.run([f"{llvm}/clang-offload-bundler", "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950",
+                        f"--input={hsaco}", f"--output={co}", "--unbundle"], check=True)
+        notes = subprocess.run([f"{llvm}/llvm-readelf", "--notes", co], capture_output=True, text=True,
+                               check=True).stdout
+    out = {}
+    for blk in notes.split("- .agpr_count")[1:]:
+        name = re.search(r"\.name:\s+(\S+)", blk).group(1)
+        out[name] = (int(re.search(r"\.vgpr_count:\s+(\d+)", blk).group(1)),
+                     int(re.search(r"\.private_segment_fixed_size:\s+(\d+)", blk).group(1)))
+    return out
+
+
+def test_hot_gemv_kernels_do_not_spill():
+    """The GEMV variants the decode shapes and the benchmark run keep every
+    value in registers: a scratch spill is a vector memory access queued
+    behind the weight loads in flight, which stalls the x staging."""
+    notes = _kernel_notes(cbuild.HSACOS["gemv"])
+    hot = [f"cima_gemv_{f}_r1_i{it}_{a}{sfx}" for f in ("q8_0", "q4_0", "q4_k", "q6_k") for it in (1, 2, 4)
+           for a in ("f32", "f16") for sfx in ("", "_epi", "_pair")]
+    hot += [f"cima_gemv_{f}_r1_i{it}_{a}_ring{e}" for f in ("q8_0", "q4_0", "q4_k", "q6_k") for it in (1, 2)
+            for a in ("f32", "f16") for e in ("", "_epi")]
+    hot += [f"cima_gemv_{f}_r1_i1_f16_{v}" for f in ("q8_0", "q4_k") for v in ("att_epi", "amax", "ring_amax")]
+    spills = {k: notes[k] for k in hot if notes[k][1] > 0}
+    assert not spills, spills
