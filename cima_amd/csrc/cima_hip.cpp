@@ -516,14 +516,14 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
         return fail(CIMA_E_INVALID, "%s: x_dtype %d / y_dtype %d not supported", api, x_dtype, y_dtype);
     if (m == 0 || n == 0) return 0;
     if (!x || !w || !y) return fail(CIMA_E_INVALID, "%s: null x, w or y", api);
-    if (!aligned(x, 8) || !aligned(w, F->w_align) || !aligned(y, 4))
-        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x 8 B, %s weights %d B, y 4 B)", api, F->name,
+    if (!aligned(x, 16) || !aligned(w, F->w_align) || !aligned(y, 4))
+        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x 16 B, %s weights %d B, y 4 B)", api, F->name,
                     F->w_align);
     // token tile (measured on MI355X, 14336x4096 Q4_K): 16 up to 16 tokens,
-    // 64 up to 256 (twice the workgroups of 128-token tiles), 128 beyond;
+    // 64 up to 128 (twice the workgroups of 128-token tiles), 128 beyond;
     // the 16-token tile stages 128 k at a time (64-row weight tiles), so it
     // needs k % 128 == 0
-    int bn = m <= 16 ? 16 : (m <= 256 ? 64 : 128);
+    int bn = m <= 16 ? 16 : (m <= 128 ? 64 : 128);
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
     if (bn == 16 && k % 128) bn = 64;
     const int bm = bn == 16 ? 64 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)

@@ -8,7 +8,7 @@
 // Each stage (BM weight rows x BK k, 8192 weights), a 256-thread workgroup
 // dequantises its weights to f16 in LDS -- bit-exact with the host
 // decoders, so the operand equals the reference's dequantised weight --
-// stages the X tile as f16 (bf16 -> f16 is exact for |x| >= 2^-14), and
+// stages the X tile as f16 (bf16 -> f16 is exact for 2^-14 <= |x| < 65520), and
 // runs v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Wave w owns weight
 // rows [w BM/4, (w+1) BM/4) of the tile and all BN tokens.  LDS is
 // double-buffered; the global loads of the next PF stages are in flight in
@@ -118,32 +118,65 @@ struct DQ6_K {
     }
 };
 
-// x element pairs (i, i+1) as loaded (f16 / bf16: one dword, f32: two), and
-// their conversion to packed f16 -- done when the stage is consumed, so the
-// loads stay in flight
-template <int XT> struct XPair { using T = uint32_t; };
-template <> struct XPair<XT_F32> { using T = float2; };
-
-// pair at element offset i: a 32-bit byte offset from the uniform base, so
-// the load takes the base in scalar registers and one vector offset (the
-// host keeps X under 4 GiB)
-template <int XT>
-DEV typename XPair<XT>::T x_pair_load(const void* x, uint32_t i) {
-    const uint8_t* b = static_cast<const uint8_t*>(x);
-    if constexpr (XT == XT_F32) return *reinterpret_cast<const float2*>(b + i * 4u);
-    else return *reinterpret_cast<const uint32_t*>(b + i * 2u);
-}
-
-template <int XT>
-DEV uint32_t x_pair_f16(const typename XPair<XT>::T& v) {
-    if constexpr (XT == XT_F16) {
-        return v;
-    } else if constexpr (XT == XT_BF16) {
-        return f2h2(__builtin_bit_cast(float, v << 16), __builtin_bit_cast(float, v & 0xffff0000u));
-    } else {
-        return f2h2(v.x, v.y);
+// x tile loads: BN tokens x BK k per stage, as 16-byte words (V elements);
+// LR = BK / V lanes cover one token's row, so each load instruction reads
+// whole rows, and load i of thread t takes token t / LR + i * 256 / LR at
+// k offset (t % LR) V (tokens past m re-read the last one; never stored
+// out).  Offsets are 32-bit bytes from the uniform base (the host keeps X
+// under 4 GiB).  Words are converted to f16 only when the stage is
+// consumed, so the loads stay in flight.
+template <int XT, int BN, int BK>
+struct XTile {
+    static constexpr int ES = XT == XT_F32 ? 4 : 2;   // bytes per element
+    static constexpr int V = 16 / ES;                 // elements per load
+    static constexpr int LR = BK / V;                 // lanes per token row
+    static constexpr int RPI = 256 / LR;              // token rows per load
+    static constexpr int NL = BN / RPI;               // loads per thread
+    static_assert(NL >= 1 && BN % RPI == 0, "tile too small for 256 threads");
+    uint4 r[NL];
+    // byte offsets of this thread's words at stage 0 and LDS slots
+    struct Map {
+        uint32_t off[NL];
+        int lds[NL];
+    };
+    DEV static Map map(int t0, int m, int k, int kp) {
+        Map mp;
+        const int tid = threadIdx.x, kk = (tid % LR) * V;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            const int tok = tid / LR + i * RPI;
+            mp.off[i] = (uint32_t)(min(t0 + tok, m - 1) * k + kk) * ES;
+            mp.lds[i] = tok * kp + kk;
+        }
+        return mp;
     }
-}
+    DEV void load(const void* x, const Map& mp, uint32_t stage_off) {
+        const uint8_t* b = static_cast<const uint8_t*>(x) + stage_off;
+#pragma unroll
+        for (int i = 0; i < NL; i++) r[i] = *reinterpret_cast<const uint4*>(b + mp.off[i]);
+    }
+    DEV void store(uint16_t* xl, const Map& mp) const {
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            uint16_t* dst = xl + mp.lds[i];
+            const uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+            if constexpr (XT == XT_F16) {
+                *reinterpret_cast<uint4*>(dst) = r[i];
+            } else if constexpr (XT == XT_BF16) {
+                // bf16 -> f16 is exact for 2^-14 <= |x| < 65520
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    o[j] = f2h2(__builtin_bit_cast(float, w[j] << 16), __builtin_bit_cast(float, w[j] & 0xffff0000u));
+                *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+            } else {
+                *reinterpret_cast<uint2*>(dst) =
+                    make_uint2(f2h2(__builtin_bit_cast(float, w[0]), __builtin_bit_cast(float, w[1])),
+                               f2h2(__builtin_bit_cast(float, w[2]), __builtin_bit_cast(float, w[3])));
+            }
+        }
+    }
+};
 
 // Tile shapes.  A stage is BM weight rows x BK k (8192 weights: one
 // 32-element sub-block per thread of the 256).  BN = 16 (up to 16 tokens)
@@ -154,7 +187,7 @@ DEV uint32_t x_pair_f16(const typename XPair<XT>::T& v) {
 template <int BN> struct GemmTile;
 template <> struct GemmTile<16> { static constexpr int BM = 64, PF = 8; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
-template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 1; };
+template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
 
 template <typename D, int BN, int XT, int YT>
 __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
@@ -174,25 +207,18 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
     // weights: thread t dequantises sub-block SPR*s + (t % SPR) of tile row t / SPR
     const int wrow = tid / SPR, wsub = tid % SPR;
     const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
-    // activations: BN x BK halves per stage, as f16 pairs
-    constexpr int XPAIRS = BN * BK / 2;
-    constexpr int XPT = (XPAIRS + 255) / 256;
+    // activations: the BN x BK tile of the stage
+    using XS = XTile<XT, BN, BK>;
+    const typename XS::Map xm = XS::map(t0, m, k, KP);
     struct Stage {
         typename D::Raw wr;
-        typename XPair<XT>::T xr[XPT];
+        XS xr;
     };
     auto issue = [&](Stage& st, int s) {
         const int sc = min(s, nk - 1);  // stages past the end re-load the last one
+        // never predicated, so the loads retire in order without a drain
         st.wr = D::load(wp, SPR * sc + wsub);
-        // never predicated (an index past the tile re-reads its last pair),
-        // so the loads retire in order without a drain
-#pragma unroll
-        for (int p = 0; p < XPT; p++) {
-            const int pi = min(tid + 256 * p, XPAIRS - 1);
-            const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
-            const int gt = min(t0 + tok, m - 1);
-            st.xr[p] = x_pair_load<XT>(x, (uint32_t)(gt * k + sc * BK + kk));
-        }
+        st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
     };
 
     float4_t acc[RA][BN / 16];
@@ -205,48 +231,51 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
 #pragma unroll
     for (int i = 0; i < PF; i++) issue(ring[i], i);
 
-    for (int base = 0; base < nk; base += PF) {
+    // one stage: dequantised weights and activations -> LDS, then (with
+    // `next`) the loads of stage s + PF into the freed slot, then the MFMAs
+    auto step = [&](Stage& st, int s, bool next) {
+        const int buf = s & 1;
+        {   // dequantised weights -> LDS
+            uint32_t o[16];
+            D::deq(st.wr, SPR * s + wsub, o);
+            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
 #pragma unroll
-        for (int b0 = 0; b0 < PF; b0++) {
-            const int s = base + b0;
-            if (s >= nk) break;
-            const int buf = s & 1;
-            Stage& st = ring[b0];
-            {   // dequantised weights -> LDS
-                uint32_t o[16];
-                D::deq(st.wr, SPR * s + wsub, o);
-                uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
+            for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        }
+        st.xr.store(xl[buf], xm);  // activations -> LDS
+        __syncthreads();
+        if (next) issue(st, s + PF);
+        // keep the loads ahead of the MFMAs (the scheduler would otherwise
+        // sink them below, leaving no load in flight during the multiply)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-            }
+        for (int ks = 0; ks < BK / 32; ks++) {
+            const int kof = 32 * ks + 8 * (lane >> 4);
+            half8_t av[RA];
 #pragma unroll
-            for (int p = 0; p < XPT; p++) {  // activations -> LDS (tokens past m are copies, never stored)
-                const int pi = tid + 256 * p;
-                if (pi < XPAIRS) {
-                    const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
-                    *reinterpret_cast<uint32_t*>(&xl[buf][tok * KP + kk]) = x_pair_f16<XT>(st.xr[p]);
-                }
-            }
-            __syncthreads();
-            issue(st, s + PF);
+            for (int a = 0; a < RA; a++)
+                av[a] = *reinterpret_cast<const half8_t*>(
+                    &wl[buf][((BM / 4) * wave + 16 * a + (lane & 15)) * KP + kof]);
 #pragma unroll
-            for (int ks = 0; ks < BK / 32; ks++) {
-                const int kof = 32 * ks + 8 * (lane >> 4);
-                half8_t av[RA];
+            for (int b = 0; b < BN / 16; b++) {
+                const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * KP + kof]);
 #pragma unroll
                 for (int a = 0; a < RA; a++)
-                    av[a] = *reinterpret_cast<const half8_t*>(
-                        &wl[buf][((BM / 4) * wave + 16 * a + (lane & 15)) * KP + kof]);
-#pragma unroll
-                for (int b = 0; b < BN / 16; b++) {
-                    const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * KP + kof]);
-#pragma unroll
-                    for (int a = 0; a < RA; a++)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
-                }
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
             }
         }
+    };
+    // whole groups of PF stages with no condition in the body (a condition
+    // would make the compiler drain every load at the loop head); stages
+    // past the end are loaded (clamped) and never consumed
+    int base = 0;
+    for (; base + PF <= nk; base += PF) {
+#pragma unroll
+        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
     }
+#pragma unroll
+    for (int b0 = 0; b0 < PF - 1; b0++)
+        if (base + b0 < nk) step(ring[b0], base + b0, false);
 
     // lane holds D[4*(lane/16) + i][lane%16] of each 16x16 tile:
     // weight row r0 + (BM/4)*wave + 16*a + 4*(lane/16) + i, token t0 + 16*b + lane%16
@@ -274,14 +303,17 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
 // of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
 // 128-row tile and tokens [wc BN/2, (wc+1) BN/2) -- so every A fragment
 // read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k
-// as in gemm_body; one (BN = 128) or two stages are in flight per
-// workgroup, and two workgroups share a CU.
+// as in gemm_body; GemmTile<BN>::PF stages are in flight per workgroup
+// (measured on MI355X, 14336x4096 Q4_K: 64 tokens 52.5 -> 49.0 us from 2
+// to 4 stages, 256 tokens 83 -> 69 us from 1 to 2), and two workgroups
+// share a CU.
 typedef float float16_t __attribute__((ext_vector_type(16)));
+
 
 template <typename D, int BN, int XT, int YT>
 __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
                                int m, int n, int k, int ldy) {
-    constexpr int BM = 128, BK = 64, KP = BK + 8, PF = BN == 64 ? 2 : 1;
+    constexpr int BM = 128, BK = 64, KP = BK + 8, PF = GemmTile<BN>::PF;
     constexpr int TB = BN / 64;  // 32-token MFMA tiles per wave
     __shared__ __align__(16) uint16_t wl[2][BM * KP];
     __shared__ __align__(16) uint16_t xl[2][BN * KP];
@@ -293,21 +325,16 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
 
     const int wrow = tid >> 1, wsub = tid & 1;
     const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
-    constexpr int XPAIRS = BN * BK / 2;
-    constexpr int XPT = XPAIRS / 256;
+    using XS = XTile<XT, BN, BK>;
+    const typename XS::Map xm = XS::map(t0, m, k, KP);
     struct Stage {
         typename D::Raw wr;
-        typename XPair<XT>::T xr[XPT];
+        XS xr;
     };
     auto issue = [&](Stage& st, int s) {
         const int sc = min(s, nk - 1);
         st.wr = D::load(wp, 2 * sc + wsub);
-#pragma unroll
-        for (int p = 0; p < XPT; p++) {
-            const int pi = tid + 256 * p;
-            const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
-            st.xr[p] = x_pair_load<XT>(x, (uint32_t)(min(t0 + tok, m - 1) * k + sc * BK + kk));
-        }
+        st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
     };
 
     float16_t acc[2][TB];
@@ -322,48 +349,48 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
 #pragma unroll
     for (int i = 0; i < PF; i++) issue(ring[i], i);
 
-    for (int base = 0; base < nk; base += PF) {
+    auto step = [&](Stage& st, int s, bool next) {
+        const int buf = s & 1;
+        {
+            uint32_t o[16];
+            D::deq(st.wr, 2 * s + wsub, o);
+            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
 #pragma unroll
-        for (int b0 = 0; b0 < PF; b0++) {
-            const int s = base + b0;
-            if (s >= nk) break;
-            const int buf = s & 1;
-            Stage& st = ring[b0];
-            {
-                uint32_t o[16];
-                D::deq(st.wr, 2 * s + wsub, o);
-                uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
+            for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        }
+        st.xr.store(xl[buf], xm);
+        __syncthreads();
+        if (next) issue(st, s + PF);
+        // keep the loads ahead of the MFMAs (the scheduler would otherwise
+        // sink them below, leaving no load in flight during the multiply)
+        __builtin_amdgcn_sched_barrier(0);
+        // lane l: A[i = l%32][k = 8(l/32) + j], B[k = 8(l/32) + j][n = l%32]
 #pragma unroll
-                for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-            }
+        for (int ks = 0; ks < BK / 16; ks++) {
+            const int kof = 16 * ks + 8 * (lane >> 5);
+            half8_t av[2], bv[TB];
 #pragma unroll
-            for (int p = 0; p < XPT; p++) {
-                const int pi = tid + 256 * p;
-                const int tok = pi / (BK / 2), kk = 2 * (pi % (BK / 2));
-                *reinterpret_cast<uint32_t*>(&xl[buf][tok * KP + kk]) = x_pair_f16<XT>(st.xr[p]);
-            }
-            __syncthreads();
-            issue(st, s + PF);
-            // lane l: A[i = l%32][k = 8(l/32) + j], B[k = 8(l/32) + j][n = l%32]
+            for (int a = 0; a < 2; a++)
+                av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(64 * wr + 32 * a + (lane & 31)) * KP + kof]);
 #pragma unroll
-            for (int ks = 0; ks < BK / 16; ks++) {
-                const int kof = 16 * ks + 8 * (lane >> 5);
-                half8_t av[2], bv[TB];
+            for (int b = 0; b < TB; b++)
+                bv[b] = *reinterpret_cast<const half8_t*>(&xl[buf][((BN / 2) * wc + 32 * b + (lane & 31)) * KP + kof]);
 #pragma unroll
-                for (int a = 0; a < 2; a++)
-                    av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(64 * wr + 32 * a + (lane & 31)) * KP + kof]);
+            for (int a = 0; a < 2; a++)
 #pragma unroll
                 for (int b = 0; b < TB; b++)
-                    bv[b] = *reinterpret_cast<const half8_t*>(
-                        &xl[buf][((BN / 2) * wc + 32 * b + (lane & 31)) * KP + kof]);
-#pragma unroll
-                for (int a = 0; a < 2; a++)
-#pragma unroll
-                    for (int b = 0; b < TB; b++)
-                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
-            }
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
+    };
+    // whole groups of PF stages, then the tail (as in gemm_body)
+    int base = 0;
+    for (; base + PF <= nk; base += PF) {
+#pragma unroll
+        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
     }
+#pragma unroll
+    for (int b0 = 0; b0 < PF - 1; b0++)
+        if (base + b0 < nk) step(ring[b0], base + b0, false);
 
     // lane l, element i of a 32x32 tile: row 8(i/4) + 4(l/32) + i%4, column l%32
     // (weight row r0 + 64 wr + 32 a + row, token t0 + (BN/2) wc + 32 b + column)

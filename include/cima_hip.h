@@ -99,7 +99,7 @@ int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
 /* Prefill GEMM tuning (no counterpart in the reference): token-tile width
  * (16, 64 or 128) for later gguf_gemm calls; 0 = the built-in choice (16 up
- * to 16 tokens, 64 up to 256, 128 beyond). */
+ * to 16 tokens, 64 up to 128, 128 beyond). */
 int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
 
 /* Fused dequant-GEMV: replaces CudaCtx::gguf_gemv (src/cuda.rs:2161-2220).
@@ -144,8 +144,8 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
  * (src/cuda.rs:2468-2570), with no slab -- W is dequantised tile by tile
  * into LDS, bit-exact f16, and multiplied with f16 MFMA, fp32 accumulate.
  * x_dtype: CIMA_DT_F32, CIMA_DT_F16 or CIMA_DT_BF16 (converted to f16;
- * exact for |x| >= 2^-14); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
- * Requires k % 64 == 0 (and k % 256 for K-quants), x 8-byte aligned. */
+ * exact for 2^-14 <= |x| < 65520); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
+ * Requires k % 64 == 0 (and k % 256 for K-quants), x 16-byte aligned. */
 int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                        int m, int n, int k, int ldy, int x_dtype, int y_dtype);
 

@@ -104,3 +104,7 @@ def test_gemm_argument_errors(hip):
     with pytest.raises(EngineError) as e:
         hip.gguf_gemm(Q4_K, x, w, y, 4, 4, 256, ldy=3)
     assert e.value.code == E_INVALID
+    xs = torch.zeros(4 * 256 + 2, device="cuda")[2:].view(4, 256)  # 8-byte aligned only
+    with pytest.raises(EngineError) as e:
+        hip.gguf_gemm(Q4_K, xs, w, y, 4, 4, 256)
+    assert e.value.code == E_INVALID
