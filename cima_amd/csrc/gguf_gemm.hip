@@ -18,6 +18,25 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 enum { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2 };
 
+// byte B of v as fp32 (v_cvt_f32_ubyte<B>: one instruction, where the
+// compiler would extract the byte first)
+template <int B>
+DEV float ubyte_f32(uint32_t v) {
+    float r;
+    if constexpr (B == 0) __asm__("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 1) __asm__("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 2) __asm__("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else __asm__("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+// the four bytes u of v as f16 pairs of s * u + t, each rounded once: with
+// s * u + t exact in fp32 (every format below) this is the host decoders'
+// value -- a product rounded once to fp32, then to f16
+DEV void bytes_affine(uint32_t v, float s, float t, uint32_t& lo, uint32_t& hi) {
+    lo = f2h2(__builtin_fmaf(s, ubyte_f32<0>(v), t), __builtin_fmaf(s, ubyte_f32<1>(v), t));
+    hi = f2h2(__builtin_fmaf(s, ubyte_f32<2>(v), t), __builtin_fmaf(s, ubyte_f32<3>(v), t));
+}
+
 // 32 contiguous elements [32j, 32j+32) of a row -> f16 bits, 2 per dword,
 // computed exactly as the host decoders do
 struct DQ8_0 {
@@ -25,13 +44,11 @@ struct DQ8_0 {
     using Raw = FQ8_0::Raw;
     DEV static Raw load(const uint8_t* row, int j) { return FQ8_0::load(row, j); }
     DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        // q = (q ^ 0x80) - 128 as unsigned bytes: d q = d u - 128 d exactly
         const float d = h2f(r.d);
         const uint32_t w[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            o[2 * i] = f2h2(d * (float)(int8_t)(w[i] & 0xff), d * (float)(int8_t)((w[i] >> 8) & 0xff));
-            o[2 * i + 1] = f2h2(d * (float)(int8_t)((w[i] >> 16) & 0xff), d * (float)(int8_t)(w[i] >> 24));
-        }
+        for (int i = 0; i < 8; i++) bytes_affine(w[i] ^ 0x80808080u, d, -128.f * d, o[2 * i], o[2 * i + 1]);
     }
 };
 struct DQ4_0 {
@@ -39,16 +56,13 @@ struct DQ4_0 {
     using Raw = FQ4_0::Raw;
     DEV static Raw load(const uint8_t* row, int j) { return FQ4_0::load(row, j); }
     DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        // byte j -> element j (low nibble), j + 16 (high); d (n - 8) exact
         const float d = h2f(r.d);
         const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-#pragma unroll
-            for (int jj = 0; jj < 2; jj++) {
-                const int b0 = (q[i] >> (16 * jj)) & 0xff, b1 = (q[i] >> (16 * jj + 8)) & 0xff;
-                o[2 * i + jj] = f2h2(d * (float)((b0 & 15) - 8), d * (float)((b1 & 15) - 8));
-                o[8 + 2 * i + jj] = f2h2(d * (float)((b0 >> 4) - 8), d * (float)((b1 >> 4) - 8));
-            }
+            bytes_affine(q[i] & 0x0F0F0F0Fu, d, -8.f * d, o[2 * i], o[2 * i + 1]);
+            bytes_affine((q[i] >> 4) & 0x0F0F0F0Fu, d, -8.f * d, o[8 + 2 * i], o[8 + 2 * i + 1]);
         }
     }
 };
@@ -73,14 +87,11 @@ struct DQ4_K {
         const float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
         const float ds = d * (float)(hi ? sc1 : sc0), mm = dmin * (float)(hi ? m1 : m0);
         const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const int sh = hi ? 4 : 0;
+        // (d*sc)*q is exact, so the subtraction is the only fp32 rounding --
+        // and a fused multiply-add rounds exactly there too
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const uint32_t n = hi ? ((q[i] >> 4) & 0x0F0F0F0Fu) : (q[i] & 0x0F0F0F0Fu);
-            // (d*sc)*q is exact, so the subtraction is the only fp32
-            // rounding -- and a fused multiply-add rounds exactly there too
-            o[2 * i] = f2h2(__builtin_fmaf(ds, (float)(n & 0xff), -mm), __builtin_fmaf(ds, (float)((n >> 8) & 0xff), -mm));
-            o[2 * i + 1] = f2h2(__builtin_fmaf(ds, (float)((n >> 16) & 0xff), -mm), __builtin_fmaf(ds, (float)(n >> 24), -mm));
-        }
+        for (int i = 0; i < 8; i++) bytes_affine((q[i] >> sh) & 0x0F0F0F0Fu, ds, -mm, o[2 * i], o[2 * i + 1]);
     }
 };
 // sub-block j: super-block j/8, r = j%8 -> half h = r/4, group g = r%4:
@@ -108,12 +119,12 @@ struct DQ6_K {
         const float ds0 = d * (float)(int8_t)(r.sc & 0xff), ds1 = d * (float)(int8_t)(r.sc >> 8);
         const uint32_t a[8] = {r.a0.x, r.a0.y, r.a0.z, r.a0.w, r.a1.x, r.a1.y, r.a1.z, r.a1.w};
         const uint32_t h[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+        // ds (u - 32) rounded once, as fma(ds, u, -32 ds) rounds it
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float ds = i < 4 ? ds0 : ds1;
             const uint32_t q = ((a[i] >> nsh) & 0x0F0F0F0Fu) | (((h[i] >> hsh) & 0x03030303u) << 4);
-            o[2 * i] = f2h2(ds * (float)((int)(q & 0xff) - 32), ds * (float)((int)((q >> 8) & 0xff) - 32));
-            o[2 * i + 1] = f2h2(ds * (float)((int)((q >> 16) & 0xff) - 32), ds * (float)((int)(q >> 24) - 32));
+            bytes_affine(q, ds, -32.f * ds, o[2 * i], o[2 * i + 1]);
         }
     }
 };

@@ -211,6 +211,10 @@ class HipCtx:
         """Override the GEMV launch plan (0, 0 = built-in heuristic)."""
         self._check(self.lib.cima_hip_set_gemv_tuning(self.handle, rows, lanes_per_row))
 
+    def set_gemm_tile(self, tokens: int = 0) -> None:
+        """Prefill GEMM token-tile width (16, 64 or 128; 0 = built-in choice)."""
+        self._check(self.lib.cima_hip_set_gemm_tile(self.handle, int(tokens)))
+
     def set_gemv_grid(self, wgs_per_cu: int = 0) -> None:
         """Cap the persistent GEMV grid at this many workgroups per CU (0 = fill)."""
         self._check(self.lib.cima_hip_set_gemv_grid(self.handle, wgs_per_cu))

@@ -108,3 +108,29 @@ def test_gemm_argument_errors(hip):
     with pytest.raises(EngineError) as e:
         hip.gguf_gemm(Q4_K, xs, w, y, 4, 4, 256)
     assert e.value.code == E_INVALID
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
+@pytest.mark.parametrize("bn", [16, 64, 128])
+def test_gemm_dequantises_bit_exactly(hip, t, bn):
+    """With X the identity, Y = dequant(W)^T: every f16 weight the kernel
+    multiplies, read back exactly (an f16 times 1.0, summed with exact
+    zeros in fp32), must equal the host decoder's f16 bits -- random block
+    bytes (scales of every exponent, NaN-free) through each token tile."""
+    k = 256
+    n = 96
+    nbytes = n * k // oracle.BLOCK_ELEMS[t] * oracle.BLOCK_BYTES[t]
+    raw = mg.xorshift_bytes(nbytes, seed=0x9E3779B97F4A7C15 + bn)
+    # half the rows with raw random scale fields, half with the scales
+    # pinned near 1 (the selftest's choice) so that no row overflows
+    w = np.concatenate([raw[:nbytes // 2], mg.sane_scales(t, raw[nbytes // 2:])]).reshape(n, -1)
+    want = oracle.f16_bits_to_f32(oracle.dequant(t, w.reshape(-1), n * k)).reshape(n, k)
+    ok = np.isfinite(want).all(axis=1)
+    x = np.eye(k, dtype=np.float32)
+    hip.set_gemm_tile(bn)
+    try:
+        y, _ = run(hip, t, w, x, k, n, k, gguf.DT_F16, gguf.DT_F32)
+    finally:
+        hip.set_gemm_tile(0)
+    got = y.T  # [n, k]
+    assert np.array_equal(got[ok], want[ok]), (int(ok.sum()), np.argwhere(got[ok] != want[ok])[:4])
