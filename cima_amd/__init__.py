@@ -1,7 +1,8 @@
 """cima_amd -- MI355X (gfx950) GGUF dequant-GEMV hot path of the cima engine.
 
 Native parts (built by ``cima_amd.build`` into ``cima_amd/lib``):
-  * ``cima_gguf.hsaco`` -- hand-written HIP kernels for gfx950
+  * ``cima_gemv_{a,b,c}.hsaco``, ``cima_gemm.hsaco``, ``cima_dequant.hsaco``,
+    ``cima_decode.hsaco`` -- hand-written HIP kernels for gfx950
   * ``libcima_hip.so``  -- the C ABI of ``include/cima_hip.h``
   * ``libcima_synth.so`` -- seeded synthetic weights (``include/cima_synth.h``)
 

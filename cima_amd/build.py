@@ -1,7 +1,7 @@
 """Build recipe for the native parts of cima_amd (runs on a CPU-only host).
 
 Produces, in ``cima_amd/lib/``:
-  cima_gemv.hsaco     gfx950 code objects (hipcc --genco): decode GEMVs,
+  cima_gemv_a/b/c.hsaco  gfx950 code objects (hipcc --genco): decode GEMVs,
   cima_gemm.hsaco       prefill dequant-GEMMs (MFMA),
   cima_dequant.hsaco    dequant-to-f16 and packed gather,
   cima_decode.hsaco     decode-step support (norm, RoPE, attention, argmax)
@@ -25,10 +25,13 @@ INCLUDE = os.path.join(ROOT, "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
-# code object -> HIP source
-SOURCES = {"gemv": "gguf_gemv.hip", "gemm": "gguf_gemm.hip", "dequant": "gguf_dequant.hip",
-           "decode": "decode_ops.hip"}
+# code object -> (HIP source, defines); the GEMVs are split over three code
+# objects by format set so that they compile in parallel
+SOURCES = {"gemv_a": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=0"]), "gemv_b": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=1"]),
+           "gemv_c": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=2"]), "gemm": ("gguf_gemm.hip", []),
+           "dequant": ("gguf_dequant.hip", []), "decode": ("decode_ops.hip", [])}
 HSACOS = {name: os.path.join(LIB, f"cima_{name}.hsaco") for name in SOURCES}
+GEMV_OBJECTS = ("gemv_a", "gemv_b", "gemv_c")
 LIBHIP = os.path.join(LIB, "libcima_hip.so")
 LIBSYNTH = os.path.join(LIB, "libcima_synth.so")
 
@@ -46,7 +49,8 @@ HIPCC_FLAGS = [
 def _cmds():
     hipcc = os.path.join(ROCM, "bin", "hipcc")
     return {
-        **{path: [hipcc, *HIPCC_FLAGS, f"-I{CSRC}", "--genco", "-o", path, os.path.join(CSRC, SOURCES[name])]
+        **{path: [hipcc, *HIPCC_FLAGS, *SOURCES[name][1], f"-I{CSRC}", "--genco", "-o", path,
+                  os.path.join(CSRC, SOURCES[name][0])]
            for name, path in HSACOS.items()},
         LIBHIP: ["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-D__HIP_PLATFORM_AMD__",
                  f"-I{INCLUDE}", f"-I{ROCM}/include", os.path.join(CSRC, "cima_hip.cpp"),

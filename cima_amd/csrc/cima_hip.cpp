@@ -45,23 +45,35 @@ struct Fmt {
     int w_align;      // required alignment of the weight base pointer
     int gemv_unit;    // elements one lane decodes per GEMV step
     int pad_shift;    // GEMV x staging: 16 B of LDS padding per 2^pad_shift elements
+    int gemv_module;  // code object holding the format's GEMVs (kModuleFiles)
 };
 
 const Fmt* fmt_of(int t) {
-    static const Fmt q8_0 = {"q8_0", 32, 34, 32, 2, 32, 5};
-    static const Fmt q4_0 = {"q4_0", 32, 18, 32, 2, 32, 5};
-    static const Fmt q4_k = {"q4_k", 256, 144, 32, 16, 64, 6};
-    static const Fmt q6_k = {"q6_k", 256, 210, 64, 2, 64, 6};
+    static const Fmt q8_0 = {"q8_0", 32, 34, 32, 2, 32, 5, 0};
+    static const Fmt q4_0 = {"q4_0", 32, 18, 32, 2, 32, 5, 0};
+    static const Fmt q4_1 = {"q4_1", 32, 20, 32, 4, 32, 5, 2};
+    static const Fmt q5_0 = {"q5_0", 32, 22, 32, 2, 32, 5, 2};
+    static const Fmt q5_1 = {"q5_1", 32, 24, 32, 8, 32, 5, 2};
+    static const Fmt q4_k = {"q4_k", 256, 144, 32, 16, 64, 6, 0};
+    static const Fmt q5_k = {"q5_k", 256, 176, 32, 16, 64, 6, 1};
+    static const Fmt q6_k = {"q6_k", 256, 210, 64, 2, 64, 6, 1};
+    static const Fmt iq4_xs = {"iq4_xs", 256, 136, 32, 8, 64, 6, 2};
     switch (t) {
     case CIMA_GGML_Q8_0: return &q8_0;
     case CIMA_GGML_Q4_0: return &q4_0;
+    case CIMA_GGML_Q4_1: return &q4_1;
+    case CIMA_GGML_Q5_0: return &q5_0;
+    case CIMA_GGML_Q5_1: return &q5_1;
     case CIMA_GGML_Q4_K: return &q4_k;
+    case CIMA_GGML_Q5_K: return &q5_k;
     case CIMA_GGML_Q6_K: return &q6_k;
+    case CIMA_GGML_IQ4_XS: return &iq4_xs;
     default: return nullptr;
     }
 }
 
-const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_K, CIMA_GGML_Q6_K};
+const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_1, CIMA_GGML_Q5_0, CIMA_GGML_Q5_1,
+                        CIMA_GGML_Q4_K, CIMA_GGML_Q5_K, CIMA_GGML_Q6_K, CIMA_GGML_IQ4_XS};
 // prefill GEMM token-tile widths the code object is built for
 const int kGemmBN[] = {16, 64, 128};
 
@@ -87,7 +99,7 @@ struct cima_hip_ctx {
     int device = 0;
     int num_cu = 0;
     int max_lds = 0;  // bytes of LDS one workgroup may use
-    hipModule_t modules[4] = {nullptr, nullptr, nullptr, nullptr};  // gemv, gemm, dequant, decode
+    hipModule_t modules[6] = {};  // kModuleFiles
     bool loaded = false;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
@@ -116,8 +128,11 @@ int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, vo
     return 0;
 }
 
-const char* const kModuleFiles[4] = {"cima_gemv.hsaco", "cima_gemm.hsaco", "cima_dequant.hsaco",
-                                     "cima_decode.hsaco"};
+// code objects: the GEMVs in three (format sets compiled in parallel),
+// the prefill GEMMs, dequant / gather, the decode-step kernels
+enum { MOD_GEMM = 3, MOD_DEQUANT = 4, MOD_DECODE = 5, NUM_MODULES = 6 };
+const char* const kModuleFiles[NUM_MODULES] = {"cima_gemv_a.hsaco", "cima_gemv_b.hsaco", "cima_gemv_c.hsaco",
+                                               "cima_gemm.hsaco", "cima_dequant.hsaco", "cima_decode.hsaco"};
 
 // decode-step kernels (cima_decode.hsaco)
 const char* const kDecodeKernels[] = {
@@ -306,7 +321,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         return hip_fail(e, "hipDeviceGetAttribute(LDS per block)");
     }
     const std::string dir = code_dir ? std::string(code_dir) : default_code_dir();
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < NUM_MODULES; i++) {
         const std::string path = dir + "/" + kModuleFiles[i];
         if ((e = hipModuleLoad(&ctx->modules[i], path.c_str())) != hipSuccess) {
             unload(ctx);
@@ -333,27 +348,27 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                         continue;  // attention / argmax variants are f16 only
                     char name[96];
                     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s", F->name, sh[0], sh[1], act, sfx);
-                    if (!rc) rc = add(0, name);
+                    if (!rc) rc = add(F->gemv_module, name);
                 }
         for (int it = 1; it <= 2; it++)
             for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"}) {
                 char name[96];
                 snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
-                if (!rc) rc = add(0, name);
+                if (!rc) rc = add(F->gemv_module, name);
             }
         for (int bn : kGemmBN)
             for (const char* xt : {"f32", "f16", "bf16"})
                 for (const char* yt : {"f32", "f16"}) {
                     char name[96];
                     snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xt, yt);
-                    if (!rc) rc = add(1, name);
+                    if (!rc) rc = add(MOD_GEMM, name);
                 }
-        if (!rc) rc = add(2, std::string("cima_dequant_") + F->name);
-        if (!rc) rc = add(2, std::string("cima_gather_") + F->name);
+        if (!rc) rc = add(MOD_DEQUANT, std::string("cima_dequant_") + F->name);
+        if (!rc) rc = add(MOD_DEQUANT, std::string("cima_gather_") + F->name);
     }
-    if (!rc) rc = add(2, "cima_stream_read");
+    if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
     for (const char* kn : kDecodeKernels)
-        if (!rc) rc = add(3, kn);
+        if (!rc) rc = add(MOD_DECODE, kn);
     if (rc) {
         unload(ctx);
         delete ctx;

@@ -42,8 +42,13 @@ __device__ void gather_body(const uint8_t* __restrict__ table, const uint32_t* _
 
 DQ_KERNELS(q8_0, FQ8_0)
 DQ_KERNELS(q4_0, FQ4_0)
+DQ_KERNELS(q4_1, FQ4_1)
+DQ_KERNELS(q5_0, FQ5_0)
+DQ_KERNELS(q5_1, FQ5_1)
 DQ_KERNELS(q4_k, FQ4_K)
+DQ_KERNELS(q5_k, FQ5_K)
 DQ_KERNELS(q6_k, FQ6_K)
+DQ_KERNELS(iq4_xs, FIQ4_XS)
 
 
 // ------------------------------------------------------ bandwidth reference

@@ -8,7 +8,8 @@
 
 #define DEV __device__ __forceinline__
 
-enum { GT_Q4_0 = 2, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q6_K = 14 };
+enum { GT_Q4_0 = 2, GT_Q4_1 = 3, GT_Q5_0 = 6, GT_Q5_1 = 7, GT_Q8_0 = 8, GT_Q4_K = 12, GT_Q5_K = 13, GT_Q6_K = 14,
+       GT_IQ4_XS = 23 };
 enum { ACT_F32 = 0, ACT_F16 = 1 };
 
 // ---------------------------------------------------------------- helpers
@@ -47,6 +48,55 @@ DEV uint32_t ld2(const uint8_t* p) {
     uint16_t v;
     __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 2);
     return v;
+}
+
+DEV uint32_t ld4u(const uint8_t* p) {
+    uint32_t v;
+    __builtin_memcpy(&v, __builtin_assume_aligned(p, 2), 4);
+    return v;
+}
+
+// byte B of v as fp32 (v_cvt_f32_ubyte<B>: one instruction, where the
+// compiler would extract the byte first)
+template <int B>
+DEV float ubyte_f32(uint32_t v) {
+    float r;
+    if constexpr (B == 0) __asm__("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 1) __asm__("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 2) __asm__("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else __asm__("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+// the four bytes u of v as f16 pairs of s * u + t, each rounded once: with
+// s * u exact in fp32 (every format here) this is the host decoders'
+// s * u + t -- rounded once to fp32, then to f16 -- where they add a term
+// (t: a min or an offset product), signs of zero included
+DEV void bytes_affine(uint32_t v, float s, float t, uint32_t& lo, uint32_t& hi) {
+    lo = f2h2(__builtin_fmaf(s, ubyte_f32<0>(v), t), __builtin_fmaf(s, ubyte_f32<1>(v), t));
+    hi = f2h2(__builtin_fmaf(s, ubyte_f32<2>(v), t), __builtin_fmaf(s, ubyte_f32<3>(v), t));
+}
+
+// the four bytes u of v as f16 pairs of s * (u - c): c and u - c exact
+// small integers, so this is the host decoders' d * q with its sign of zero
+// (an fma of s u - s c would give +0 where d * 0 is -0)
+DEV void bytes_scaled(uint32_t v, float s, float c, uint32_t& lo, uint32_t& hi) {
+    lo = f2h2(s * (ubyte_f32<0>(v) - c), s * (ubyte_f32<1>(v) - c));
+    hi = f2h2(s * (ubyte_f32<2>(v) - c), s * (ubyte_f32<3>(v) - c));
+}
+
+// bits 0..3 of b -> bit 4 of bytes 0..3 (the 5th bits of four elements):
+// the four shifted copies of b in the product never overlap
+DEV uint32_t spread4(uint32_t b) { return ((b * 0x00204081u) & 0x01010101u) << 4; }
+
+// IQ4_XS: the four nibbles (one per byte, 0..15) of n -> their codebook
+// values (ggml kvalues_iq4nl, src/quant.rs:817-822) as int8 bytes: two
+// byte permutes over the 16-entry table, then a per-byte select on bit 3
+DEV uint32_t iq4nl_bytes(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(0xF6EADDCFu, 0xBFAD9881u, sel);  // entries 0..7
+    const uint32_t hi = __builtin_amdgcn_perm(0x71594535u, 0x26190D01u, sel);  // entries 8..15
+    const uint32_t m = ((n >> 3) & 0x01010101u) * 0xFFu;
+    return (hi & m) | (lo & ~m);
 }
 
 DEV void store32h(uint16_t* out, const uint32_t (&o)[16]) {
@@ -116,6 +166,93 @@ struct FQ4_0 {
                 o[8 + 2 * i + j] = f2h2(h0, h1);
             }
         }
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
+};
+
+// --------------------------------------------------------- format: Q4_1
+// block (20 B): f16 d, f16 m, u8 qs[16]; byte j = elem j (low nibble),
+// elem j+16 (high); x = d * q + m   (src/quant.rs:646-669)
+struct FQ4_1 {
+    static constexpr int BE = 32, BB = 20, UE = 32, UPB = 1;
+    struct Raw { uint4 q; uint32_t dm; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 20;
+        Raw r;
+        r.dm = ld4u(blk);
+        r.q = ld16u(blk + 4);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int, uint16_t* out) {
+        const float d = h2f(r.dm & 0xffffu), m = h2f(r.dm >> 16);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        uint32_t o[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bytes_affine(q[i] & 0x0F0F0F0Fu, d, m, o[2 * i], o[2 * i + 1]);
+            bytes_affine((q[i] >> 4) & 0x0F0F0F0Fu, d, m, o[8 + 2 * i], o[8 + 2 * i + 1]);
+        }
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
+};
+
+// --------------------------------------------------------- format: Q5_0
+// block (22 B): f16 d, u32 qh (bit e = element e's 5th bit), u8 qs[16];
+// x = d * (q5 - 16)   (src/quant.rs:671-699)
+struct FQ5_0 {
+    static constexpr int BE = 32, BB = 22, UE = 32, UPB = 1;
+    struct Raw { uint4 q; uint32_t d, qh; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 22;
+        Raw r;
+        r.d = ld2(blk);
+        r.qh = ld4u(blk + 2);
+        r.q = ld16u(blk + 6);
+        return r;
+    }
+    // the 32 5-bit quants, one per byte in element order (q5[0..3] =
+    // elements 0..15, q5[4..7] = 16..31)
+    DEV static void q5(uint4 qv, uint32_t qh, uint32_t (&o)[8]) {
+        const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[i] = (q[i] & 0x0F0F0F0Fu) | spread4((qh >> (4 * i)) & 15u);
+            o[4 + i] = ((q[i] >> 4) & 0x0F0F0F0Fu) | spread4((qh >> (16 + 4 * i)) & 15u);
+        }
+    }
+    DEV static void dequant(const Raw& r, int, uint16_t* out) {
+        const float d = h2f(r.d);
+        uint32_t v[8], o[16];
+        q5(r.q, r.qh, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) bytes_scaled(v[i], d, 16.f, o[2 * i], o[2 * i + 1]);
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
+};
+
+// --------------------------------------------------------- format: Q5_1
+// block (24 B): f16 d, f16 m, u32 qh, u8 qs[16]; x = d * q5 + m
+// (src/quant.rs:701-729)
+struct FQ5_1 {
+    static constexpr int BE = 32, BB = 24, UE = 32, UPB = 1;
+    struct Raw { uint4 q; uint32_t dm, qh; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)u * 24;
+        Raw r;
+        r.dm = ld4u(blk);
+        r.qh = ld4u(blk + 4);
+        r.q = ld16u(blk + 8);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int, uint16_t* out) {
+        const float d = h2f(r.dm & 0xffffu), m = h2f(r.dm >> 16);
+        uint32_t v[8], o[16];
+        FQ5_0::q5(r.q, r.qh, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) bytes_affine(v[i], d, m, o[2 * i], o[2 * i + 1]);
         store32h(out, o);
     }
     DEV static int out_elem(int u) { return u * 32; }
@@ -196,6 +333,86 @@ struct FQ4_K {
         ph[1] = make_uint4(oh[4], oh[5], oh[6], oh[7]);
     }
     DEV static int out_elem(int u) { return elem0(u); }
+};
+
+// --------------------------------------------------------- format: Q5_K
+// super-block (176 B): f16 d, f16 dmin, u8 scales[12] (as Q4_K), u8 qh[32],
+// u8 qs[128] (Q4_K's nibble layout); chunk c's low / high nibbles take bit
+// 2c / 2c+1 of qh[l] as +16; x = (d*sc)*q5 - dmin*m  (src/quant.rs:776-815).
+// Unit u as FQ4_K's, plus qh bytes [16*(u%2), +16).
+struct FQ5_K {
+    static constexpr int BE = 256, BB = 176, UE = 32, UPB = 8;
+    struct Raw { uint4 h, q, qh; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 176;
+        Raw r;
+        r.h = ld16a(blk);
+        r.qh = ld16a(blk + 16 + (u & 1) * 16);
+        r.q = ld16a(blk + 48 + (u & 7) * 16);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int u, uint16_t* out) {
+        const int c = (u & 7) >> 1;
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(r.h, c, sc0, m0, sc1, m1);
+        const float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
+        const float d0 = d * (float)sc0, mm0 = dmin * (float)m0, d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        const uint32_t h[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+        uint32_t ol[8], oh[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (((h[i] >> (2 * c)) & 0x01010101u) << 4);
+            const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((h[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            // (d*sc)*q5 is exact, so the subtraction is the one fp32 rounding
+            bytes_affine(lo, d0, -mm0, ol[2 * i], ol[2 * i + 1]);
+            bytes_affine(hi, d1, -mm1, oh[2 * i], oh[2 * i + 1]);
+        }
+        uint4* pl = reinterpret_cast<uint4*>(out);
+        uint4* ph = reinterpret_cast<uint4*>(out + 32);
+        pl[0] = make_uint4(ol[0], ol[1], ol[2], ol[3]);
+        pl[1] = make_uint4(ol[4], ol[5], ol[6], ol[7]);
+        ph[0] = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+        ph[1] = make_uint4(oh[4], oh[5], oh[6], oh[7]);
+    }
+    DEV static int out_elem(int u) { return FQ4_K::elem0(u); }
+};
+
+// ------------------------------------------------------- format: IQ4_XS
+// super-block (136 B): f16 d, u16 scales_h (2 bits per sub-block), u8
+// scales_l[4] (4 bits per sub-block), u8 qs[128]; sub-block ib (32
+// elements) = qs[16 ib, +16): low nibbles elements 0..15, high 16..31;
+// x = (d (ls - 32)) * codebook[q]   (src/quant.rs:823-854).  Unit u =
+// sub-block u % 8 of super-block u / 8.
+DEV float iq4xs_dl(uint2 hdr, int ib) {
+    const uint32_t ls = ((hdr.y >> (4 * ib)) & 15u) | (((hdr.x >> (16 + 2 * ib)) & 3u) << 4);
+    return h2f(hdr.x & 0xffffu) * (float)((int)ls - 32);  // exact: 11-bit x 6-bit
+}
+struct FIQ4_XS {
+    static constexpr int BE = 256, BB = 136, UE = 32, UPB = 8;
+    struct Raw { uint4 q; uint2 hdr; };
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 3) * 136;
+        Raw r;
+        r.hdr = *reinterpret_cast<const uint2*>(blk);
+        r.q = ld16u(blk + 8 + (u & 7) * 16);
+        return r;
+    }
+    DEV static void dequant(const Raw& r, int u, uint16_t* out) {
+        const float dl = iq4xs_dl(r.hdr, u & 7);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        uint32_t o[16];
+        // codebook values are int8: v = (v ^ 0x80) - 128 as unsigned bytes
+        // (dl v is exact: a 17-bit by 7-bit product)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bytes_scaled(iq4nl_bytes(q[i] & 0x0F0F0F0Fu) ^ 0x80808080u, dl, 128.f, o[2 * i], o[2 * i + 1]);
+            bytes_scaled(iq4nl_bytes((q[i] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u, dl, 128.f, o[8 + 2 * i],
+                         o[8 + 2 * i + 1]);
+        }
+        store32h(out, o);
+    }
+    DEV static int out_elem(int u) { return u * 32; }
 };
 
 // --------------------------------------------------------- format: Q6_K

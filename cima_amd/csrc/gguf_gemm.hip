@@ -1,3 +1,5 @@
+#include <type_traits>
+
 #include "gguf_formats.h"
 
 // ------------------------------------------------------- prefill GEMM (MFMA)
@@ -18,27 +20,11 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 enum { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2 };
 
-// byte B of v as fp32 (v_cvt_f32_ubyte<B>: one instruction, where the
-// compiler would extract the byte first)
-template <int B>
-DEV float ubyte_f32(uint32_t v) {
-    float r;
-    if constexpr (B == 0) __asm__("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 1) __asm__("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 2) __asm__("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-    else __asm__("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-// the four bytes u of v as f16 pairs of s * u + t, each rounded once: with
-// s * u + t exact in fp32 (every format below) this is the host decoders'
-// value -- a product rounded once to fp32, then to f16
-DEV void bytes_affine(uint32_t v, float s, float t, uint32_t& lo, uint32_t& hi) {
-    lo = f2h2(__builtin_fmaf(s, ubyte_f32<0>(v), t), __builtin_fmaf(s, ubyte_f32<1>(v), t));
-    hi = f2h2(__builtin_fmaf(s, ubyte_f32<2>(v), t), __builtin_fmaf(s, ubyte_f32<3>(v), t));
-}
-
 // 32 contiguous elements [32j, 32j+32) of a row -> f16 bits, 2 per dword,
-// computed exactly as the host decoders do
+// the values of the host decoders (formats whose decoders multiply only,
+// d * (q - c), use fma(d, q, -c d) here: the same value, though a zero
+// weight may come out +0 where the decoder gives -0 -- a difference no
+// product sum shows)
 struct DQ8_0 {
     static constexpr int BE = 32, BB = 34;
     using Raw = FQ8_0::Raw;
@@ -63,6 +49,91 @@ struct DQ4_0 {
         for (int i = 0; i < 4; i++) {
             bytes_affine(q[i] & 0x0F0F0F0Fu, d, -8.f * d, o[2 * i], o[2 * i + 1]);
             bytes_affine((q[i] >> 4) & 0x0F0F0F0Fu, d, -8.f * d, o[8 + 2 * i], o[8 + 2 * i + 1]);
+        }
+    }
+};
+struct DQ4_1 {
+    static constexpr int BE = 32, BB = 20;
+    using Raw = FQ4_1::Raw;
+    DEV static Raw load(const uint8_t* row, int j) { return FQ4_1::load(row, j); }
+    DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        // d q + m: the product is exact, the sum rounded once
+        const float d = h2f(r.dm & 0xffffu), m = h2f(r.dm >> 16);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bytes_affine(q[i] & 0x0F0F0F0Fu, d, m, o[2 * i], o[2 * i + 1]);
+            bytes_affine((q[i] >> 4) & 0x0F0F0F0Fu, d, m, o[8 + 2 * i], o[8 + 2 * i + 1]);
+        }
+    }
+};
+template <bool MIN>
+struct DQ5_01 {
+    static constexpr int BE = 32, BB = MIN ? 24 : 22;
+    using FQ = typename std::conditional<MIN, FQ5_1, FQ5_0>::type;
+    using Raw = typename FQ::Raw;
+    DEV static Raw load(const uint8_t* row, int j) { return FQ::load(row, j); }
+    DEV static void deq(const Raw& r, int, uint32_t (&o)[16]) {
+        uint32_t v[8];
+        FQ5_0::q5(r.q, r.qh, v);
+        float d, t;
+        if constexpr (MIN) {
+            d = h2f(r.dm & 0xffffu);
+            t = h2f(r.dm >> 16);   // d q5 + m
+        } else {
+            d = h2f(r.d);
+            t = -16.f * d;         // d (q5 - 16), exact
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) bytes_affine(v[i], d, t, o[2 * i], o[2 * i + 1]);
+    }
+};
+// sub-block j: super-block j/8, s = j%8 -> chunk c = s/2 of Q4_K's nibble
+// layout (low nibbles if s is even) with 5th bits = bit s of qh[l]
+struct DQ5_K {
+    static constexpr int BE = 256, BB = 176;
+    struct Raw { uint4 h, q0, q1, qh0, qh1; };
+    DEV static Raw load(const uint8_t* row, int j) {
+        const uint8_t* blk = row + (size_t)(j >> 3) * 176;
+        const int c = (j & 7) >> 1;
+        Raw r;
+        r.h = ld16a(blk);
+        r.qh0 = ld16a(blk + 16);
+        r.qh1 = ld16a(blk + 32);
+        r.q0 = ld16a(blk + 48 + 32 * c);
+        r.q1 = ld16a(blk + 64 + 32 * c);
+        return r;
+    }
+    DEV static void deq(const Raw& r, int j, uint32_t (&o)[16]) {
+        const int s = j & 7, c = s >> 1;
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scales(r.h, c, sc0, m0, sc1, m1);
+        const bool hi = s & 1;
+        const float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
+        const float ds = d * (float)(hi ? sc1 : sc0), mm = dmin * (float)(hi ? m1 : m0);
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t h[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
+        const int sh = hi ? 4 : 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t n = ((q[i] >> sh) & 0x0F0F0F0Fu) | (((h[i] >> s) & 0x01010101u) << 4);
+            bytes_affine(n, ds, -mm, o[2 * i], o[2 * i + 1]);  // (d sc) q5 exact; one rounding
+        }
+    }
+};
+// sub-block j: super-block j/8, ib = j%8: codebook values of qs[16 ib, +16)
+struct DIQ4_XS {
+    static constexpr int BE = 256, BB = 136;
+    using Raw = FIQ4_XS::Raw;
+    DEV static Raw load(const uint8_t* row, int j) { return FIQ4_XS::load(row, j); }
+    DEV static void deq(const Raw& r, int j, uint32_t (&o)[16]) {
+        const float dl = iq4xs_dl(r.hdr, j & 7);
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bytes_affine(iq4nl_bytes(q[i] & 0x0F0F0F0Fu) ^ 0x80808080u, dl, -128.f * dl, o[2 * i], o[2 * i + 1]);
+            bytes_affine(iq4nl_bytes((q[i] >> 4) & 0x0F0F0F0Fu) ^ 0x80808080u, dl, -128.f * dl, o[8 + 2 * i],
+                         o[8 + 2 * i + 1]);
         }
     }
 };
@@ -443,5 +514,10 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
 
 GEMM_FMT(q8_0, DQ8_0)
 GEMM_FMT(q4_0, DQ4_0)
+GEMM_FMT(q4_1, DQ4_1)
+GEMM_FMT(q5_0, DQ5_01<false>)
+GEMM_FMT(q5_1, DQ5_01<true>)
 GEMM_FMT(q4_k, DQ4_K)
+GEMM_FMT(q5_k, DQ5_K)
 GEMM_FMT(q6_k, DQ6_K)
+GEMM_FMT(iq4_xs, DIQ4_XS)

@@ -14,6 +14,8 @@
 //   _ring  item-ring main loop (deeper prefetch; tall one-unit-row matrices)
 //   _epi   bias and/or residual (mode 1) operands present
 // Every variant can take an RMSNorm prologue (GemvExt::norm_w).
+#include <type_traits>
+
 #include "gguf_formats.h"
 
 // ------------------------------------------------------ reductions (wave64)
@@ -126,6 +128,61 @@ struct IQ4_0 {
     }
 };
 
+// Q4_1 unit = 1 block: sum (d q + m) x = d sum q x + m sum x.
+struct IQ4_1 {
+    static constexpr int BE = 32, BB = 20, UE = 32, PADSH = 5;
+    using Raw = FQ4_1::Raw;
+    using Xf = IQ4_0::Xf;
+    DEV static Raw load(const uint8_t* row, int u) { return FQ4_1::load(row, u); }
+    DEV static void loadx(const uint8_t* xq, const float* xs, const float* xsum, int u, Xf& f) {
+        IQ4_0::loadx(xq, xs, xsum, u, f);
+    }
+    DEV static float dot(const Raw& r, const Xf& f, int) {
+        const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+        int sh = 0, sl = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t lo = q[i] & 0x0F0F0F0Fu, hi = (q[i] >> 4) & 0x0F0F0F0Fu;
+            sh = dot4(lo, f.h[i], sh);
+            sl = dot4(lo, f.l[i], sl);
+            sh = dot4(hi, f.h[4 + i], sh);
+            sl = dot4(hi, f.l[4 + i], sl);
+        }
+        return fmaf(h2f(r.dm & 0xffffu) * f.s, fix16(sh, sl), h2f(r.dm >> 16) * f.sum);
+    }
+};
+
+// Q5_0 / Q5_1 unit = 1 block: the 5-bit quants (0..31) dot x;
+// Q5_0: d (sum q5 x - 16 sum x), Q5_1: d sum q5 x + m sum x.
+template <bool MIN>
+struct IQ5_01 {
+    static constexpr int BE = 32, BB = MIN ? 24 : 22, UE = 32, PADSH = 5;
+    using FQ = typename std::conditional<MIN, FQ5_1, FQ5_0>::type;
+    using Raw = typename FQ::Raw;
+    using Xf = IQ4_0::Xf;
+    DEV static Raw load(const uint8_t* row, int u) { return FQ::load(row, u); }
+    DEV static void loadx(const uint8_t* xq, const float* xs, const float* xsum, int u, Xf& f) {
+        IQ4_0::loadx(xq, xs, xsum, u, f);
+    }
+    DEV static float dot(const Raw& r, const Xf& f, int) {
+        uint32_t v[8];
+        FQ5_0::q5(r.q, r.qh, v);
+        int sh = 0, sl = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sh = dot4(v[i], f.h[i], sh);
+            sl = dot4(v[i], f.l[i], sl);
+        }
+        if constexpr (MIN) {
+            return fmaf(h2f(r.dm & 0xffffu) * f.s, fix16(sh, sl), h2f(r.dm >> 16) * f.sum);
+        } else {
+            return h2f(r.d) * fmaf(f.s, fix16(sh, sl), -16.f * f.sum);
+        }
+    }
+};
+using IQ5_0 = IQ5_01<false>;
+using IQ5_1 = IQ5_01<true>;
+
 // Q4_K unit = one 64-element chunk c of a super-block: 32 qs bytes whose low
 // nibbles are sub-block 2c and high nibbles sub-block 2c+1, plus the header.
 struct IQ4_K {
@@ -165,6 +222,88 @@ struct IQ4_K {
         const float pos = fmaf((float)(sc & 0xff) * f.s0, fix16(h0, l0), ((float)((sc >> 8) & 0xff) * f.s1) * fix16(h1, l1));
         const float neg = fmaf((float)(m & 0xff), f.sum0, (float)((m >> 8) & 0xff) * f.sum1);
         return fmaf(d, pos, -dmin * neg);
+    }
+};
+
+// Q5_K unit = IQ4_K's 64-element chunk, each quant lifted by its 5th bit
+// (bits 2c / 2c+1 of the 32 qh bytes).
+struct IQ5_K {
+    static constexpr int BE = 256, BB = 176, UE = 64, PADSH = 6;
+    struct Raw { uint4 h, q0, q1, qh0, qh1; };
+    using Xf = IQ4_K::Xf;
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 2) * 176;
+        Raw r;
+        r.h = ld16a(blk);
+        r.qh0 = ld16a(blk + 16);
+        r.qh1 = ld16a(blk + 32);
+        r.q0 = ld16a(blk + 48 + (u & 3) * 32);
+        r.q1 = ld16a(blk + 64 + (u & 3) * 32);
+        return r;
+    }
+    DEV static void loadx(const uint8_t* xq, const float* xs, const float* xsum, int u, Xf& f) {
+        IQ4_K::loadx(xq, xs, xsum, u, f);
+    }
+    DEV static float dot(const Raw& r, const Xf& f, int u) {
+        const uint32_t q[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t qh[8] = {r.qh0.x, r.qh0.y, r.qh0.z, r.qh0.w, r.qh1.x, r.qh1.y, r.qh1.z, r.qh1.w};
+        const int c = u & 3;
+        int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c)) & 0x01010101u) << 4);
+            const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            h0 = dot4(lo, f.h[i], h0);
+            l0 = dot4(lo, f.l[i], l0);
+            h1 = dot4(hi, f.h[8 + i], h1);
+            l1 = dot4(hi, f.l[8 + i], l1);
+        }
+        uint32_t sc, m;
+        q4k_scale_pair(r.h, q4k_sel(c), sc, m);
+        const float d = h2f(r.h.x & 0xffffu), dmin = h2f(r.h.x >> 16);
+        const float pos = fmaf((float)(sc & 0xff) * f.s0, fix16(h0, l0), ((float)((sc >> 8) & 0xff) * f.s1) * fix16(h1, l1));
+        const float neg = fmaf((float)(m & 0xff), f.sum0, (float)((m >> 8) & 0xff) * f.sum1);
+        return fmaf(d, pos, -dmin * neg);
+    }
+};
+
+// IQ4_XS unit = 64 elements = sub-blocks 2(u%4), 2(u%4)+1: 32 qs bytes
+// (each sub-block's low nibbles then high nibbles in element order) as
+// codebook int8 values dot x, times the sub-block scales d (ls - 32).
+struct IIQ4_XS {
+    static constexpr int BE = 256, BB = 136, UE = 64, PADSH = 6;
+    struct Raw { uint4 q0, q1; uint2 hdr; };
+    using Xf = IQ4_K::Xf;
+    DEV static Raw load(const uint8_t* row, int u) {
+        const uint8_t* blk = row + (size_t)(u >> 2) * 136;
+        Raw r;
+        r.hdr = *reinterpret_cast<const uint2*>(blk);
+        r.q0 = ld16u(blk + 8 + (u & 3) * 32);
+        r.q1 = ld16u(blk + 24 + (u & 3) * 32);
+        return r;
+    }
+    DEV static void loadx(const uint8_t* xq, const float* xs, const float* xsum, int u, Xf& f) {
+        IQ4_K::loadx(xq, xs, xsum, u, f);
+    }
+    DEV static float dot(const Raw& r, const Xf& f, int u) {
+        // x chunks 4u..4u+3 = sub-block A low, A high, B low, B high
+        const uint32_t a[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w}, b[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        int h0 = 0, l0 = 0, h1 = 0, l1 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t al = iq4nl_bytes(a[i] & 0x0F0F0F0Fu), ah = iq4nl_bytes((a[i] >> 4) & 0x0F0F0F0Fu);
+            const uint32_t bl = iq4nl_bytes(b[i] & 0x0F0F0F0Fu), bh = iq4nl_bytes((b[i] >> 4) & 0x0F0F0F0Fu);
+            h0 = dot4(al, f.h[i], h0);
+            l0 = dot4(al, f.l[i], l0);
+            h0 = dot4(ah, f.h[4 + i], h0);
+            l0 = dot4(ah, f.l[4 + i], l0);
+            h1 = dot4(bl, f.h[8 + i], h1);
+            l1 = dot4(bl, f.l[8 + i], l1);
+            h1 = dot4(bh, f.h[12 + i], h1);
+            l1 = dot4(bh, f.l[12 + i], l1);
+        }
+        const int ib = 2 * (u & 3);
+        return fmaf(iq4xs_dl(r.hdr, ib) * f.s0, fix16(h0, l0), (iq4xs_dl(r.hdr, ib + 1) * f.s1) * fix16(h1, l1));
     }
 };
 
@@ -839,8 +978,21 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_ACT(FN, F, 1, 1) GEMV_ACT(FN, F, 1, 2) GEMV_ACT(FN, F, 1, 4) GEMV_ACT(FN, F, 1, 8)   \
     GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F)
 
+// the formats of this code object: the file is compiled once per set (in
+// parallel), each set to its own code object
+#if !defined(CIMA_GEMV_SET)
+#error "CIMA_GEMV_SET (0, 1 or 2) selects the formats of this code object"
+#elif CIMA_GEMV_SET == 0
 GEMV_FMT(q8_0, IQ8_0)
 GEMV_FMT(q4_0, IQ4_0)
 GEMV_FMT(q4_k, IQ4_K)
+#elif CIMA_GEMV_SET == 1
 GEMV_FMT(q6_k, IQ6_K)
+GEMV_FMT(q5_k, IQ5_K)
+#else
+GEMV_FMT(q4_1, IQ4_1)
+GEMV_FMT(q5_0, IQ5_0)
+GEMV_FMT(q5_1, IQ5_1)
+GEMV_FMT(iq4_xs, IIQ4_XS)
+#endif
 

@@ -116,7 +116,67 @@ void quant_q4_0(const float* x, uint8_t* blk) {
     for (int j = 0; j < 16; j++) blk[2 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
 }
 
-void quant_q4_k(const float* x, uint8_t* blk) {
+void quant_q4_1(const float* x, uint8_t* blk) {
+    float mn = x[0], mx = x[0];
+    for (int i = 1; i < 32; i++) {
+        mn = std::min(mn, x[i]);
+        mx = std::max(mx, x[i]);
+    }
+    uint16_t dh = to_f16((mx - mn) / 15.f), mh = to_f16(mn);
+    float d = from_f16(dh), m = from_f16(mh);
+    put16(blk, dh);
+    put16(blk + 2, mh);
+    int q[32];
+    for (int i = 0; i < 32; i++) q[i] = d > 0.f ? std::min(15, std::max(0, iround((x[i] - m) / d))) : 0;
+    for (int j = 0; j < 16; j++) blk[4 + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
+}
+
+// 5-bit quants q[32] -> qh (bit e = q[e] bit 4) and the nibble bytes
+void pack_q5(const int* q, uint8_t* qh4, uint8_t* qs) {
+    uint32_t qh = 0;
+    for (int e = 0; e < 32; e++) qh |= (uint32_t)((q[e] >> 4) & 1) << e;
+    for (int i = 0; i < 4; i++) qh4[i] = (uint8_t)(qh >> (8 * i));
+    for (int j = 0; j < 16; j++) qs[j] = (uint8_t)((q[j] & 15) | ((q[j + 16] & 15) << 4));
+}
+
+void quant_q5_0(const float* x, uint8_t* blk) {
+    float amax = 0.f, vmax = 0.f;
+    for (int i = 0; i < 32; i++)
+        if (fabsf(x[i]) > amax) {
+            amax = fabsf(x[i]);
+            vmax = x[i];
+        }
+    uint16_t dh = to_f16(vmax / -16.f);
+    float d = from_f16(dh);
+    put16(blk, dh);
+    int q[32];
+    for (int i = 0; i < 32; i++) q[i] = d != 0.f ? std::min(31, std::max(0, iround(x[i] / d) + 16)) : 16;
+    pack_q5(q, blk + 2, blk + 6);
+}
+
+void quant_q5_1(const float* x, uint8_t* blk) {
+    float mn = x[0], mx = x[0];
+    for (int i = 1; i < 32; i++) {
+        mn = std::min(mn, x[i]);
+        mx = std::max(mx, x[i]);
+    }
+    uint16_t dh = to_f16((mx - mn) / 31.f), mh = to_f16(mn);
+    float d = from_f16(dh), m = from_f16(mh);
+    put16(blk, dh);
+    put16(blk + 2, mh);
+    int q[32];
+    for (int i = 0; i < 32; i++) q[i] = d > 0.f ? std::min(31, std::max(0, iround((x[i] - m) / d))) : 0;
+    pack_q5(q, blk + 4, blk + 8);
+}
+
+// Q4_K / Q5_K: per 32-element sub-block a min/max fit to 0..LEVELS, the
+// 6-bit scales and mins relative to the super-block's d and dmin; Q5_K adds
+// the quants' 5th bits (bit 2c / 2c+1 of qh[l] for chunk c's low / high
+// nibbles)
+template <int LEVELS>
+void quant_kq(const float* x, uint8_t* blk) {
+    constexpr bool Q5 = LEVELS == 31;
+    constexpr int BB = Q5 ? 176 : 144;
     float scale[8], minv[8];
     float max_scale = 0.f, max_min = 0.f;
     for (int j = 0; j < 8; j++) {
@@ -125,7 +185,7 @@ void quant_q4_k(const float* x, uint8_t* blk) {
             mn = std::min(mn, x[32 * j + i]);
             mx = std::max(mx, x[32 * j + i]);
         }
-        scale[j] = (mx - mn) / 15.f;
+        scale[j] = (mx - mn) / (float)LEVELS;
         minv[j] = -mn;
         max_scale = std::max(max_scale, scale[j]);
         max_min = std::max(max_min, minv[j]);
@@ -137,7 +197,7 @@ void quant_q4_k(const float* x, uint8_t* blk) {
         sc[j] = d > 0.f ? std::min(63, std::max(0, iround(scale[j] / d))) : 0;
         m[j] = dmin > 0.f ? std::min(63, std::max(0, iround(minv[j] / dmin))) : 0;
     }
-    memset(blk, 0, 144);
+    memset(blk, 0, BB);
     put16(blk, dh);
     put16(blk + 2, mh);
     uint8_t* s = blk + 4;
@@ -154,11 +214,65 @@ void quant_q4_k(const float* x, uint8_t* blk) {
     for (int j = 0; j < 8; j++) {
         float ds = d * (float)sc[j], dm = dmin * (float)m[j];
         for (int i = 0; i < 32; i++)
-            q[32 * j + i] = ds > 0.f ? std::min(15, std::max(0, iround((x[32 * j + i] + dm) / ds))) : 0;
+            q[32 * j + i] = ds > 0.f ? std::min(LEVELS, std::max(0, iround((x[32 * j + i] + dm) / ds))) : 0;
     }
-    uint8_t* qs = blk + 16;
+    uint8_t* qs = blk + (Q5 ? 48 : 16);
     for (int c = 0; c < 4; c++)
-        for (int i = 0; i < 32; i++) qs[c * 32 + i] = (uint8_t)(q[c * 64 + i] | (q[c * 64 + 32 + i] << 4));
+        for (int i = 0; i < 32; i++)
+            qs[c * 32 + i] = (uint8_t)((q[c * 64 + i] & 15) | ((q[c * 64 + 32 + i] & 15) << 4));
+    if (Q5) {
+        uint8_t* qh = blk + 16;
+        for (int c = 0; c < 4; c++)
+            for (int l = 0; l < 32; l++)
+                qh[l] |= (uint8_t)((((q[c * 64 + l] >> 4) & 1) << (2 * c)) | (((q[c * 64 + 32 + l] >> 4) & 1) << (2 * c + 1)));
+    }
+}
+void quant_q4_k(const float* x, uint8_t* blk) { quant_kq<15>(x, blk); }
+void quant_q5_k(const float* x, uint8_t* blk) { quant_kq<31>(x, blk); }
+
+// IQ4_XS: per sub-block the largest-magnitude value maps to the codebook's
+// -127 end; the sub-block scales become 6-bit steps (ls - 32) of the
+// super-block d, and each value takes the nearest codebook entry
+const float kIQ4NL[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                          1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+void quant_iq4_xs(const float* x, uint8_t* blk) {
+    float dl[8], amax_dl = 0.f;
+    for (int ib = 0; ib < 8; ib++) {
+        float amax = 0.f, vmax = 0.f;
+        for (int i = 0; i < 32; i++)
+            if (fabsf(x[32 * ib + i]) > amax) {
+                amax = fabsf(x[32 * ib + i]);
+                vmax = x[32 * ib + i];
+            }
+        dl[ib] = vmax / -127.f;
+        amax_dl = std::max(amax_dl, fabsf(dl[ib]));
+    }
+    uint16_t dh = to_f16(amax_dl / 31.f);
+    float d = from_f16(dh);
+    memset(blk, 0, 136);
+    put16(blk, dh);
+    uint16_t scales_h = 0;
+    for (int ib = 0; ib < 8; ib++) {
+        int ls = d > 0.f ? std::min(63, std::max(0, iround(dl[ib] / d) + 32)) : 32;
+        scales_h |= (uint16_t)(((ls >> 4) & 3) << (2 * ib));
+        blk[4 + ib / 2] |= (uint8_t)((ls & 15) << (4 * (ib % 2)));
+        float dq = d * (float)(ls - 32);
+        int q[32];
+        for (int i = 0; i < 32; i++) {
+            int best = 0;
+            float be = INFINITY;
+            for (int j = 0; j < 16; j++) {
+                float e = fabsf(dq * kIQ4NL[j] - x[32 * ib + i]);
+                if (e < be) {
+                    be = e;
+                    best = j;
+                }
+            }
+            q[i] = best;
+        }
+        for (int j = 0; j < 16; j++) blk[8 + 16 * ib + j] = (uint8_t)(q[j] | (q[j + 16] << 4));
+    }
+    put16(blk + 2, scales_h);
 }
 
 // sub-block j (16 elements) of a Q6_K super-block holds elements
@@ -208,8 +322,13 @@ bool qfmt(int t, QFmt* f) {
     switch (t) {
     case 8: *f = {32, 34, quant_q8_0}; return true;
     case 2: *f = {32, 18, quant_q4_0}; return true;
+    case 3: *f = {32, 20, quant_q4_1}; return true;
+    case 6: *f = {32, 22, quant_q5_0}; return true;
+    case 7: *f = {32, 24, quant_q5_1}; return true;
     case 12: *f = {256, 144, quant_q4_k}; return true;
+    case 13: *f = {256, 176, quant_q5_k}; return true;
     case 14: *f = {256, 210, quant_q6_k}; return true;
+    case 23: *f = {256, 136, quant_iq4_xs}; return true;
     default: return false;
     }
 }

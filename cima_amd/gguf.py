@@ -14,9 +14,14 @@ class DType(enum.IntEnum):
     """GGUF block formats by ggml tensor type id."""
 
     Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
+    IQ4_XS = 23
 
     @property
     def block_elems(self) -> int:
@@ -27,8 +32,10 @@ class DType(enum.IntEnum):
         return _BLOCK_BYTES[self]
 
 
-_BLOCK_ELEMS = {DType.Q8_0: 32, DType.Q4_0: 32, DType.Q4_K: 256, DType.Q6_K: 256}
-_BLOCK_BYTES = {DType.Q8_0: 34, DType.Q4_0: 18, DType.Q4_K: 144, DType.Q6_K: 210}
+_BLOCK_ELEMS = {DType.Q8_0: 32, DType.Q4_0: 32, DType.Q4_1: 32, DType.Q5_0: 32, DType.Q5_1: 32,
+                DType.Q4_K: 256, DType.Q5_K: 256, DType.Q6_K: 256, DType.IQ4_XS: 256}
+_BLOCK_BYTES = {DType.Q8_0: 34, DType.Q4_0: 18, DType.Q4_1: 20, DType.Q5_0: 22, DType.Q5_1: 24,
+                DType.Q4_K: 144, DType.Q5_K: 176, DType.Q6_K: 210, DType.IQ4_XS: 136}
 
 # activation / output element types of the C ABI
 DT_F32, DT_F16, DT_BF16 = 0, 1, 2

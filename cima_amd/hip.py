@@ -24,7 +24,10 @@ from . import gguf
 PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_DIR = os.path.join(PKG, "lib")
 LIBHIP = os.path.join(LIB_DIR, "libcima_hip.so")
-CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco") for n in ("gemv", "gemm", "dequant", "decode")]
+# the gfx950 code objects cima_hip_init loads (names as cima_amd/build.py
+# writes them)
+CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco")
+                for n in ("gemv_a", "gemv_b", "gemv_c", "gemm", "dequant", "decode")]
 
 # declared in include/cima_hip.h, in order
 EXPORTS = (

@@ -15,7 +15,8 @@
  * last failure on the calling thread.
  *
  * Formats are ggml tensor type ids (src/formats.rs:90-117): 8 = Q8_0,
- * 2 = Q4_0, 12 = Q4_K, 14 = Q6_K.
+ * 2 = Q4_0, 3 = Q4_1, 6 = Q5_0, 7 = Q5_1, 12 = Q4_K, 13 = Q5_K, 14 = Q6_K,
+ * 23 = IQ4_XS -- every GGUF block format the reference executes.
  */
 #ifndef CIMA_HIP_H
 #define CIMA_HIP_H
@@ -28,9 +29,14 @@ extern "C" {
 
 /* ggml tensor type ids */
 #define CIMA_GGML_Q4_0 2
+#define CIMA_GGML_Q4_1 3
+#define CIMA_GGML_Q5_0 6
+#define CIMA_GGML_Q5_1 7
 #define CIMA_GGML_Q8_0 8
 #define CIMA_GGML_Q4_K 12
+#define CIMA_GGML_Q5_K 13
 #define CIMA_GGML_Q6_K 14
+#define CIMA_GGML_IQ4_XS 23
 
 /* activation / output element types */
 #define CIMA_DT_F32 0
@@ -47,7 +53,7 @@ typedef struct cima_hip_ctx cima_hip_ctx;
 
 /* Context creation: replaces CudaCtx::init (src/cuda.rs:691-908) -- device
  * selection, one non-blocking stream, then loading the prebuilt gfx950 code
- * objects (cima_gemv.hsaco, cima_gemm.hsaco, cima_dequant.hsaco,
+ * objects (cima_gemv_a/b/c.hsaco, cima_gemm.hsaco, cima_dequant.hsaco,
  * cima_decode.hsaco) with
  * hipModuleLoad and resolving every kernel (the reference JIT-compiles with
  * NVRTC and resolves its KernelSet, src/cuda.rs:808-877).

@@ -14,9 +14,10 @@
  *                        (reference test src/quant.rs:1171-1204), and numpy's
  *                        IEEE float16 cast over all f16 values and 1e6 random
  *                        f32 (independent library oracle).
- *   dequant_q8_0/q4_0/q4_k/q6_k
+ *   dequant_q8_0/q4_0/q4_1/q5_0/q5_1/q4_k/q5_k/q6_k/iq4_xs
  *                        reference known-answer tests src/quant.rs:1011,1027,
- *                        1075,1220 restated in tests/test_oracle.py; an
+ *                        1075,1101,1140,1220,1245,1261,1281 restated in
+ *                        tests/test_oracle.py; an
  *                        independent numpy decoder (tests/golden/make_golden.py)
  *                        that computes each value in float64 and rounds once
  *                        to float16 (closed form: every product is exact);
@@ -39,7 +40,8 @@
 #endif
 
 /* ggml tensor type ids, src/formats.rs:90-117 */
-enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q6_K = 14 };
+enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q4_K = 12,
+       T_Q5_K = 13, T_Q6_K = 14, T_IQ4_XS = 23 };
 
 /* ---------------------------------------------------------------------- */
 /* f16 primitives: src/traits.rs:832-854 (f16_to_f32), :857-896 (f32_to_f16) */
@@ -100,8 +102,8 @@ static inline float d16(const uint8_t* b) { return oracle_f16_to_f32((uint16_t)(
 
 int oracle_block_elems(int t) {
     switch (t) {
-    case T_Q8_0: case T_Q4_0: return 32;
-    case T_Q4_K: case T_Q6_K: return 256;
+    case T_Q8_0: case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1: return 32;
+    case T_Q4_K: case T_Q5_K: case T_Q6_K: case T_IQ4_XS: return 256;
     default: return 0;
     }
 }
@@ -110,8 +112,13 @@ int oracle_block_bytes(int t) {
     switch (t) {
     case T_Q8_0: return 34;
     case T_Q4_0: return 18;
+    case T_Q4_1: return 20;
+    case T_Q5_0: return 22;
+    case T_Q5_1: return 24;
     case T_Q4_K: return 144;
+    case T_Q5_K: return 176;
     case T_Q6_K: return 210;
+    case T_IQ4_XS: return 136;
     default: return 0;
     }
 }
@@ -148,6 +155,61 @@ int oracle_dequant_q4_0(const uint8_t* src, size_t src_len, size_t numel, uint16
             uint8_t q = blk[2 + j];
             out[b * 32 + j] = oracle_f32_to_f16(d * (float)((int)(q & 0x0F) - 8));
             out[b * 32 + j + 16] = oracle_f32_to_f16(d * (float)((int)(q >> 4) - 8));
+        }
+    }
+    return 0;
+}
+
+/* src/quant.rs:646-669: x = d q + m (the product is exact; the sum is
+ * rounded once to fp32) */
+int oracle_dequant_q4_1(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
+    size_t blocks = numel / 32;
+    if (src_len < blocks * 20 || numel % 32) return -1;
+    for (size_t b = 0; b < blocks; b++) {
+        const uint8_t* blk = src + b * 20;
+        float d = d16(blk), m = d16(blk + 2);
+        for (int j = 0; j < 16; j++) {
+            uint8_t q = blk[4 + j];
+            out[b * 32 + j] = oracle_f32_to_f16(d * (float)(q & 0x0F) + m);
+            out[b * 32 + j + 16] = oracle_f32_to_f16(d * (float)(q >> 4) + m);
+        }
+    }
+    return 0;
+}
+
+/* src/quant.rs:671-699: bit j of qh is element j's 5th bit, bit j + 16
+ * element j + 16's; x = d (q5 - 16) */
+int oracle_dequant_q5_0(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
+    size_t blocks = numel / 32;
+    if (src_len < blocks * 22 || numel % 32) return -1;
+    for (size_t b = 0; b < blocks; b++) {
+        const uint8_t* blk = src + b * 22;
+        float d = d16(blk);
+        uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) | ((uint32_t)blk[5] << 24);
+        for (int j = 0; j < 16; j++) {
+            uint8_t q = blk[6 + j];
+            uint32_t hi0 = ((qh >> j) << 4) & 0x10, hi1 = (qh >> (j + 12)) & 0x10;
+            int x0 = (int)((q & 0x0F) | hi0) - 16, x1 = (int)((q >> 4) | hi1) - 16;
+            out[b * 32 + j] = oracle_f32_to_f16(d * (float)x0);
+            out[b * 32 + j + 16] = oracle_f32_to_f16(d * (float)x1);
+        }
+    }
+    return 0;
+}
+
+/* src/quant.rs:701-729: Q5_0's bits with a min; x = d q5 + m */
+int oracle_dequant_q5_1(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
+    size_t blocks = numel / 32;
+    if (src_len < blocks * 24 || numel % 32) return -1;
+    for (size_t b = 0; b < blocks; b++) {
+        const uint8_t* blk = src + b * 24;
+        float d = d16(blk), m = d16(blk + 2);
+        uint32_t qh = (uint32_t)blk[4] | ((uint32_t)blk[5] << 8) | ((uint32_t)blk[6] << 16) | ((uint32_t)blk[7] << 24);
+        for (int j = 0; j < 16; j++) {
+            uint8_t q = blk[8 + j];
+            uint32_t hi0 = ((qh >> j) << 4) & 0x10, hi1 = (qh >> (j + 12)) & 0x10;
+            out[b * 32 + j] = oracle_f32_to_f16(d * (float)((q & 0x0F) | hi0) + m);
+            out[b * 32 + j + 16] = oracle_f32_to_f16(d * (float)((q >> 4) | hi1) + m);
         }
     }
     return 0;
@@ -194,6 +256,64 @@ int oracle_dequant_q4_k(const uint8_t* src, size_t src_len, size_t numel, uint16
     return 0;
 }
 
+/* src/quant.rs:776-815: Q4_K's layout plus qh[32]; chunk c's low and high
+ * nibbles take bits 2c and 2c + 1 of qh[l] as +16 */
+int oracle_dequant_q5_k(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
+    size_t blocks = numel / 256;
+    if (src_len < blocks * 176 || numel % 256) return -1;
+    for (size_t b = 0; b < blocks; b++) {
+        const uint8_t* blk = src + b * 176;
+        float d = d16(blk), dmin = d16(blk + 2);
+        const uint8_t* scales = blk + 4;
+        const uint8_t* qh = blk + 16;
+        const uint8_t* ql = blk + 48;
+        for (int c = 0; c < 4; c++) {
+            float sc0, m0, sc1, m1;
+            scale_min_k4(2 * c, scales, &sc0, &m0);
+            scale_min_k4(2 * c + 1, scales, &sc1, &m1);
+            float d1 = d * sc0, mm1 = dmin * m0, d2 = d * sc1, mm2 = dmin * m1;
+            uint8_t u1 = (uint8_t)(1u << (2 * c)), u2 = (uint8_t)(2u << (2 * c));
+            for (int l = 0; l < 32; l++) {
+                float hi1 = (qh[l] & u1) ? 16.0f : 0.0f, hi2 = (qh[l] & u2) ? 16.0f : 0.0f;
+                uint8_t q = ql[c * 32 + l];
+                float lo = d1 * ((float)(q & 0x0F) + hi1);
+                float hi = d2 * ((float)(q >> 4) + hi2);
+                out[b * 256 + c * 64 + l] = oracle_f32_to_f16(lo - mm1);
+                out[b * 256 + c * 64 + 32 + l] = oracle_f32_to_f16(hi - mm2);
+            }
+        }
+    }
+    return 0;
+}
+
+/* src/quant.rs:817-822: ggml's kvalues_iq4nl codebook */
+static const float IQ4NL[16] = {-127.f, -104.f, -83.f, -65.f, -49.f, -35.f, -22.f, -10.f,
+                                1.f,    13.f,   25.f,  38.f,  53.f,  69.f,  89.f,  113.f};
+
+/* src/quant.rs:823-854: 6-bit sub-block scales split over scales_h (2 bits
+ * each) and scales_l (4 bits each); x = (d (ls - 32)) codebook[q] */
+int oracle_dequant_iq4_xs(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
+    size_t blocks = numel / 256;
+    if (src_len < blocks * 136 || numel % 256) return -1;
+    for (size_t b = 0; b < blocks; b++) {
+        const uint8_t* blk = src + b * 136;
+        float d = d16(blk);
+        uint32_t scales_h = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8);
+        const uint8_t* scales_l = blk + 4;
+        const uint8_t* qs = blk + 8;
+        for (int ib = 0; ib < 8; ib++) {
+            int ls = (int)((scales_l[ib / 2] >> (4 * (ib % 2))) & 0x0F) | ((int)((scales_h >> (2 * ib)) & 3) << 4);
+            float dl = d * (float)(ls - 32);
+            const uint8_t* q = qs + ib * 16;
+            for (int j = 0; j < 16; j++) {
+                out[b * 256 + ib * 32 + j] = oracle_f32_to_f16(dl * IQ4NL[q[j] & 0x0F]);
+                out[b * 256 + ib * 32 + 16 + j] = oracle_f32_to_f16(dl * IQ4NL[q[j] >> 4]);
+            }
+        }
+    }
+    return 0;
+}
+
 /* src/quant.rs:857-896 */
 int oracle_dequant_q6_k(const uint8_t* src, size_t src_len, size_t numel, uint16_t* out) {
     size_t blocks = numel / 256;
@@ -231,8 +351,13 @@ int oracle_dequant(int t, const uint8_t* src, size_t src_len, size_t numel, uint
     switch (t) {
     case T_Q8_0: return oracle_dequant_q8_0(src, src_len, numel, out);
     case T_Q4_0: return oracle_dequant_q4_0(src, src_len, numel, out);
+    case T_Q4_1: return oracle_dequant_q4_1(src, src_len, numel, out);
+    case T_Q5_0: return oracle_dequant_q5_0(src, src_len, numel, out);
+    case T_Q5_1: return oracle_dequant_q5_1(src, src_len, numel, out);
     case T_Q4_K: return oracle_dequant_q4_k(src, src_len, numel, out);
+    case T_Q5_K: return oracle_dequant_q5_k(src, src_len, numel, out);
     case T_Q6_K: return oracle_dequant_q6_k(src, src_len, numel, out);
+    case T_IQ4_XS: return oracle_dequant_iq4_xs(src, src_len, numel, out);
     default: return -2;
     }
 }

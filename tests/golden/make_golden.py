@@ -22,8 +22,11 @@ import os
 
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-BLOCK = {Q8_0: (32, 34), Q4_0: (32, 18), Q4_K: (256, 144), Q6_K: (256, 210)}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 2, 3, 6, 7, 8, 12, 13, 14, 23
+BLOCK = {Q8_0: (32, 34), Q4_0: (32, 18), Q4_1: (32, 20), Q5_0: (32, 22), Q5_1: (32, 24), Q4_K: (256, 144),
+         Q5_K: (256, 176), Q6_K: (256, 210), IQ4_XS: (256, 136)}
+# ggml's kvalues_iq4nl
+IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.float64)
 HERE = os.path.dirname(os.path.abspath(__file__))
 GOLDEN = os.path.join(HERE, "gguf_golden.npz")
 
@@ -73,7 +76,32 @@ def decode_exact(t: int, src: np.ndarray) -> np.ndarray:
             qs = b[:, 2:18]
             q = np.concatenate([qs & 15, qs >> 4], axis=1).astype(np.float64) - 8.0
             v = d[:, None] * q
-        elif t == Q4_K:
+        elif t in (Q4_1, Q5_0, Q5_1):
+            # 32 elements: nibble bytes (low = element j, high = j + 16), a
+            # 5th bit per element from a 32-bit mask (bit e = element e)
+            d = _f16(b, 0)
+            qoff = {Q4_1: 4, Q5_0: 6, Q5_1: 8}[t]
+            qs = b[:, qoff:qoff + 16].astype(np.int64)
+            q = np.concatenate([qs & 15, qs >> 4], axis=1)
+            if t != Q4_1:
+                hoff = 2 if t == Q5_0 else 4
+                qh = b[:, hoff:hoff + 4].copy().view("<u4")[:, 0].astype(np.int64)
+                q = q | (((qh[:, None] >> np.arange(32)[None, :]) & 1) << 4)
+            if t == Q5_0:
+                v = d[:, None] * (q - 16).astype(np.float64)      # no min term (keeps -0)
+            else:
+                v = d[:, None] * q.astype(np.float64) + _f16(b, 2)[:, None]
+        elif t == IQ4_XS:
+            d = _f16(b, 0)
+            sh = b[:, 2:4].copy().view("<u2")[:, 0].astype(np.int64)
+            sl = b[:, 4:8].astype(np.int64)
+            ib = np.arange(8)
+            ls = ((sl[:, ib // 2] >> (4 * (ib % 2))) & 15) | (((sh[:, None] >> (2 * ib)) & 3) << 4)
+            qs = b[:, 8:136].reshape(nb, 8, 16).astype(np.int64)
+            q = np.concatenate([qs & 15, qs >> 4], axis=2)            # sub-block, 32 elements
+            v = (d[:, None, None] * (ls - 32)[:, :, None]) * IQ4NL[q]
+            v = v.reshape(nb, 256)
+        elif t in (Q4_K, Q5_K):
             d, dmin = _f16(b, 0), _f16(b, 2)
             s = b[:, 4:16].astype(np.int64)
             # 6-bit (scale, min) of sub-blocks 0..7
@@ -82,9 +110,14 @@ def decode_exact(t: int, src: np.ndarray) -> np.ndarray:
             mn[:, :4] = s[:, 4:8] & 63
             sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
             mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
-            qs = b[:, 16:144].reshape(nb, 4, 32)
+            qs = b[:, 16:144].reshape(nb, 4, 32) if t == Q4_K else b[:, 48:176].reshape(nb, 4, 32)
             # chunk c: low nibbles -> sub-block 2c, high nibbles -> 2c+1
-            q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.float64)
+            q = np.stack([qs & 15, qs >> 4], axis=2).reshape(nb, 8, 32).astype(np.int64)
+            if t == Q5_K:
+                # sub-block j's 5th bits: bit j of qh[l] (l = 0..31)
+                qh = b[:, 16:48].astype(np.int64)
+                q = q | (((qh[:, None, :] >> np.arange(8)[None, :, None]) & 1) << 4)
+            q = q.astype(np.float64)
             v = (d[:, None, None] * sc[:, :, None]) * q - (dmin[:, None] * mn)[:, :, None]
             v = v.reshape(nb, 256)
         elif t == Q6_K:
@@ -113,7 +146,7 @@ def sane_scales(t: int, blocks: np.ndarray) -> np.ndarray:
     reference's GEMV selftest does (src/selftest.rs:1042-1063)."""
     be, bb = BLOCK[t]
     b = blocks.reshape(-1, bb).copy()
-    offs = [208] if t == Q6_K else ([0, 2] if t == Q4_K else [0])
+    offs = {Q6_K: [208], Q4_K: [0, 2], Q5_K: [0, 2], Q4_1: [0, 2], Q5_1: [0, 2]}.get(t, [0])
     for o in offs:
         h = b[:, o:o + 2].copy().view("<u2")[:, 0]
         h = (h & 0x83FF) | (14 << 10)
@@ -128,7 +161,8 @@ def gemv64(w16: np.ndarray, x: np.ndarray, n: int, k: int) -> np.ndarray:
 
 def make() -> dict:
     out = {}
-    for t, name in ((Q8_0, "q8_0"), (Q4_0, "q4_0"), (Q4_K, "q4_k"), (Q6_K, "q6_k")):
+    for t, name in ((Q8_0, "q8_0"), (Q4_0, "q4_0"), (Q4_1, "q4_1"), (Q5_0, "q5_0"), (Q5_1, "q5_1"), (Q4_K, "q4_k"),
+                    (Q5_K, "q5_k"), (Q6_K, "q6_k"), (IQ4_XS, "iq4_xs")):
         be, bb = BLOCK[t]
         nblocks = 24 if be == 256 else 64
         src = xorshift_bytes(nblocks * bb, seed=0x9E3779B97F4A7C15 + t)

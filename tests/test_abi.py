@@ -14,7 +14,7 @@ from cima_amd import hip as hipmod
 from cima_amd import build as cbuild
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-FORMATS = [gguf.DType.Q8_0, gguf.DType.Q4_0, gguf.DType.Q4_K, gguf.DType.Q6_K]
+FORMATS = list(gguf.DType)
 
 
 def header_functions(path):
@@ -44,8 +44,9 @@ def test_code_object_holds_every_kernel():
         assert blob[:4] == b"\x7fELF" or blob.startswith(b"__CLANG_OFFLOAD_BUNDLE__")
         assert b"gfx950" in blob
         blobs[name] = blob
-    for f in ("q8_0", "q4_0", "q4_k", "q6_k"):
-        blob = blobs["gemv"]
+    gemv = b"".join(blobs[o] for o in cbuild.GEMV_OBJECTS)
+    for f in [t.name.lower() for t in FORMATS]:
+        blob = gemv
         for r, it in ((1, 1), (1, 2), (1, 4), (1, 8), (2, 1), (2, 2), (2, 4)):
             for a in ("f32", "f16"):
                 for sfx in ("", "_epi", "_pair", "_pair_epi") + (("_att_epi", "_amax") if a == "f16" else ()):
@@ -127,7 +128,7 @@ def test_format_tables_match_oracle(t):
     for numel in (0, 256, 4096, 14336 * 4096):
         assert gguf.storage_bytes(t, numel) == oracle.storage_bytes(t, numel)
     with pytest.raises(ValueError):
-        gguf.storage_bytes(13, 256)
+        gguf.storage_bytes(10, 256)
 
 
 def test_synth_normal_is_deterministic_and_normal():
@@ -140,7 +141,9 @@ def test_synth_normal_is_deterministic_and_normal():
 
 
 # relative normwise quantisation error bounds of the synthetic quantisers
-QERR = {gguf.DType.Q8_0: 0.01, gguf.DType.Q4_0: 0.2, gguf.DType.Q4_K: 0.12, gguf.DType.Q6_K: 0.04}
+QERR = {gguf.DType.Q8_0: 0.01, gguf.DType.Q4_0: 0.2, gguf.DType.Q4_1: 0.12, gguf.DType.Q5_0: 0.08,
+        gguf.DType.Q5_1: 0.07, gguf.DType.Q4_K: 0.12, gguf.DType.Q5_K: 0.07, gguf.DType.Q6_K: 0.04,
+        gguf.DType.IQ4_XS: 0.12}
 
 
 @pytest.mark.parametrize("t", FORMATS, ids=lambda t: t.name)
@@ -160,7 +163,7 @@ def test_synth_rejects_bad_shapes():
     with pytest.raises(ValueError):
         synth.quantize(12, np.zeros((2, 100), np.float32))
     with pytest.raises(ValueError):
-        synth.weights(13, 1, 0.02, 2, 256)
+        synth.weights(10, 1, 0.02, 2, 256)
 
 
 def _kernel_notes(hsaco):
@@ -191,11 +194,20 @@ def test_hot_gemv_kernels_do_not_spill():
     """The GEMV variants the decode shapes and the benchmark run keep every
     value in registers: a scratch spill is a vector memory access queued
     behind the weight loads in flight, which stalls the x staging."""
-    notes = _kernel_notes(cbuild.HSACOS["gemv"])
-    hot = [f"cima_gemv_{f}_r1_i{it}_{a}{sfx}" for f in ("q8_0", "q4_0", "q4_k", "q6_k") for it in (1, 2, 4)
+    notes = {}
+    for o in cbuild.GEMV_OBJECTS:
+        notes.update(_kernel_notes(cbuild.HSACOS[o]))
+    fmts = [t.name.lower() for t in FORMATS]
+    hot = [f"cima_gemv_{f}_r1_i{it}_{a}{sfx}" for f in fmts for it in (1, 2, 4)
            for a in ("f32", "f16") for sfx in ("", "_epi", "_pair")]
-    hot += [f"cima_gemv_{f}_r1_i{it}_{a}_ring{e}" for f in ("q8_0", "q4_0", "q4_k", "q6_k") for it in (1, 2)
+    hot += [f"cima_gemv_{f}_r1_i{it}_{a}_ring{e}" for f in fmts for it in (1, 2)
             for a in ("f32", "f16") for e in ("", "_epi")]
     hot += [f"cima_gemv_{f}_r1_i1_f16_{v}" for f in ("q8_0", "q4_k") for v in ("att_epi", "amax", "ring_amax")]
     spills = {k: notes[k] for k in hot if notes[k][1] > 0}
     assert not spills, spills
+
+
+def test_python_binding_checks_every_code_object():
+    """HipCtx refuses to start without any of the code objects the build
+    writes (the list the C library loads)."""
+    assert sorted(hipmod.CODE_OBJECTS) == sorted(cbuild.HSACOS.values())

@@ -16,9 +16,10 @@ from cima_amd.hip import EngineError, E_INVALID
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-FORMATS = [Q8_0, Q4_0, Q4_K, Q6_K]
-NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 2, 3, 6, 7, 8, 12, 13, 14, 23
+FORMATS = [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K, IQ4_XS]
+NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q4_K: "q4_k", Q5_K: "q5_k",
+         Q6_K: "q6_k", IQ4_XS: "iq4_xs"}
 TDT = {gguf.DT_F32: torch.float32, gguf.DT_F16: torch.float16, gguf.DT_BF16: torch.bfloat16}
 
 

@@ -19,9 +19,10 @@ from cima_amd.hip import EngineError, E_INVALID, E_FORMAT
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
-Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
-FORMATS = [Q8_0, Q4_0, Q4_K, Q6_K]
-NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS = 2, 3, 6, 7, 8, 12, 13, 14, 23
+FORMATS = [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K, IQ4_XS]
+NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q4_K: "q4_k", Q5_K: "q5_k",
+         Q6_K: "q6_k", IQ4_XS: "iq4_xs"}
 fid = [NAMES[t] for t in FORMATS]
 
 
@@ -163,6 +164,11 @@ BASELINE_SHAPES = [
     (Q8_0, 151936, 896),    # config 5: tied Qwen2.5-0.5B head
     (Q8_0, 4096, 4096),
     (Q4_0, 4096, 4096),
+    (Q5_K, 14336, 4096),    # the other formats of Q4_K_M / IQ4_XS files
+    (IQ4_XS, 4096, 14336),
+    (Q5_0, 4864, 896),
+    (Q5_1, 896, 4864),
+    (Q4_1, 1152, 896),
 ]
 
 
@@ -311,7 +317,7 @@ def test_gemv_argument_errors(hip):
             hip.gguf_gemv(Q4_K, x, w, None, y, 4, a["k"], a["mode"])
         assert e.value.code == E_INVALID and not e.value.fatal
     with pytest.raises(EngineError) as e:
-        hip.gguf_gemv(13, x, w, None, y, 4, 256, 0)  # Q5_K: not built here
+        hip.gguf_gemv(10, x, w, None, y, 4, 256, 0)  # Q2_K: not a format the reference executes
     assert e.value.code == E_FORMAT
     with pytest.raises(EngineError) as e:
         hip.gguf_gemv(Q4_K, x.data_ptr() + 4, w, None, y, 1, 128 * 2, 0)  # x not 16-B aligned
@@ -398,7 +404,7 @@ def test_item_ring_matches_double_buffer(t):
         finally:
             del os.environ["CIMA_GEMV_RING"]
         ctxs[mode].use_torch_stream()
-    be = {2: 32, 8: 32, 12: 256, 14: 256}[t]
+    be = mg.BLOCK[t][0]
     ue = 64 if be == 256 else 32  # elements per unit
     # one unit per lane at 32 lanes; two per lane at 64 (ragged: 100 units)
     for n, k in ((1, 32 * ue), (37, 32 * ue), (1000, 32 * ue), (37, 128 * ue), (300, 100 * ue)):

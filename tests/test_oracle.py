@@ -12,8 +12,10 @@ import oracle
 import make_golden as mg
 
 Q4_0, Q8_0, Q4_K, Q6_K = oracle.Q4_0, oracle.Q8_0, oracle.Q4_K, oracle.Q6_K
-FORMATS = [Q8_0, Q4_0, Q4_K, Q6_K]
-NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_K: "q4_k", Q6_K: "q6_k"}
+Q4_1, Q5_0, Q5_1, Q5_K, IQ4_XS = oracle.Q4_1, oracle.Q5_0, oracle.Q5_1, oracle.Q5_K, oracle.IQ4_XS
+FORMATS = [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4_K, Q5_K, Q6_K, IQ4_XS]
+NAMES = {Q8_0: "q8_0", Q4_0: "q4_0", Q4_1: "q4_1", Q5_0: "q5_0", Q5_1: "q5_1", Q4_K: "q4_k", Q5_K: "q5_k",
+         Q6_K: "q6_k", IQ4_XS: "iq4_xs"}
 
 
 def f16le(v: float) -> bytes:
@@ -105,6 +107,85 @@ def test_q4_0_nibble_order_and_offset():
         assert abs(out[j + 16] - 0.25 * ((15 - j) - 8)) < 1e-3
 
 
+def test_q4_1_scale_plus_min():
+    """src/quant.rs:1245-1259"""
+    blk = bytearray(20)
+    blk[0:2] = f16le(0.5)
+    blk[2:4] = f16le(-1.5)
+    for j in range(16):
+        blk[4 + j] = j | ((15 - j) << 4)
+    out = oracle.f16_bits_to_f32(oracle.dequant(Q4_1, np.frombuffer(bytes(blk), np.uint8), 32))
+    for j in range(16):
+        assert abs(out[j] - (0.5 * j - 1.5)) < 1e-3
+        assert abs(out[j + 16] - (0.5 * (15 - j) - 1.5)) < 1e-3
+
+
+def test_q5_0_fifth_bit_mapping():
+    """src/quant.rs:1261-1279: bit r of qh is element r's 5th bit (exact
+    values, so equality)"""
+    blk = bytearray(22)
+    blk[0:2] = f16le(1.0)
+    qh = 0xA5F00F5A
+    blk[2:6] = qh.to_bytes(4, "little")
+    for j in range(16):
+        blk[6 + j] = (j % 16) | ((j % 16) << 4)
+    out = oracle.f16_bits_to_f32(oracle.dequant(Q5_0, np.frombuffer(bytes(blk), np.uint8), 32))
+    for r in range(32):
+        assert out[r] == (r % 16) + ((qh >> r) & 1) * 16 - 16, r
+
+
+def test_q5_1_fifth_bit_plus_min():
+    """src/quant.rs:1281-1305 (exact values here, so equality)"""
+    blk = bytearray(24)
+    blk[0:2] = f16le(0.5)
+    blk[2:4] = f16le(2.0)
+    qh = 0x1234ABCD
+    blk[4:8] = qh.to_bytes(4, "little")
+    for j in range(16):
+        blk[8 + j] = j | ((15 - j) << 4)
+    out = oracle.f16_bits_to_f32(oracle.dequant(Q5_1, np.frombuffer(bytes(blk), np.uint8), 32))
+    for r in range(32):
+        nib = r if r < 16 else 15 - (r - 16)
+        assert out[r] == 0.5 * (nib + ((qh >> r) & 1) * 16) + 2.0, r
+
+
+def test_q5_k_fifth_bit_and_rotating_masks():
+    """src/quant.rs:1101-1138: d = 1, dmin = 0, scales 1; qh bit 2 lifts
+    chunk 1's low half by 16 and leaves chunk 0 alone"""
+    blk = bytearray(176)
+    blk[0:2] = f16le(1.0)
+    blk[2:4] = f16le(0.0)
+    for j in range(4):
+        blk[4 + j] = 1
+        blk[4 + j + 4] = 0
+    for j in range(4, 8):
+        blk[4 + j + 4] = 1
+    for i in range(128):
+        blk[48 + i] = (i % 16) | ((i % 16) << 4)
+    for i in range(32):
+        blk[16 + i] = 0b0000_0100
+    out = oracle.f16_bits_to_f32(oracle.dequant(Q5_K, np.frombuffer(bytes(blk), np.uint8), 256))
+    for l in range(32):
+        nib = l % 16
+        assert out[l] == nib, l
+        assert out[64 + l] == nib + 16, l
+
+
+def test_iq4_xs_codebook_and_split_scales():
+    """src/quant.rs:1140-1169: sub-block 0 scale 33 (ls - 32 = 1) from
+    scales_l's low nibble 1 and scales_h bits 10b; sub-block 1 scale 0 -> -32"""
+    blk = bytearray(136)
+    blk[0:2] = f16le(1.0)
+    blk[2] = 0b0000_0010
+    blk[4] = 0x01
+    for i in range(16):
+        blk[8 + i] = (i % 16) | ((i % 16) << 4)
+    out = oracle.f16_bits_to_f32(oracle.dequant(IQ4_XS, np.frombuffer(bytes(blk), np.uint8), 256))
+    for j in range(16):
+        assert out[j] == mg.IQ4NL[j], j
+    assert out[32] == -32.0 * mg.IQ4NL[0]
+
+
 def test_f16_converters_are_ieee_exact():
     """src/quant.rs:1171-1204: exhaustive round trip, NaN class, RTNE ties."""
     h = np.arange(65536, dtype=np.uint16)
@@ -124,10 +205,15 @@ def test_f16_converters_are_ieee_exact():
 
 
 def test_storage_sizes_match_ggml():
-    """src/quant.rs:1207-1218 (the formats this build executes)"""
+    """src/quant.rs:1207-1218"""
     assert oracle.storage_bytes(Q8_0, 1024) == 1024 // 32 * 34
     assert oracle.storage_bytes(Q4_0, 1024) == 1024 // 32 * 18
+    assert oracle.storage_bytes(Q4_1, 1024) == 1024 // 32 * 20
+    assert oracle.storage_bytes(Q5_0, 1024) == 1024 // 32 * 22
+    assert oracle.storage_bytes(Q5_1, 1024) == 1024 // 32 * 24
     assert oracle.storage_bytes(Q4_K, 1024) == 1024 // 256 * 144
+    assert oracle.storage_bytes(Q5_K, 1024) == 1024 // 256 * 176
+    assert oracle.storage_bytes(IQ4_XS, 1024) == 1024 // 256 * 136
     assert oracle.storage_bytes(Q6_K, 1024) == 1024 // 256 * 210
 
 
@@ -208,7 +294,7 @@ def test_dequant_size_mismatch_errors(t):
 
 def test_unsupported_format_rejected():
     with pytest.raises(ValueError):
-        oracle.dequant(13, np.zeros(176, np.uint8), 256)  # Q5_K: not executed by this build
+        oracle.dequant(10, np.zeros(84, np.uint8), 256)  # Q2_K: not a format the reference executes
 
 
 # ----------------------------------------------------------- gemv / gemm
