@@ -260,7 +260,8 @@ def main():
         ctx_len = 2048
         for i in range(dcfg.n_layers):
             dd.load_kv(i, *synthetic_kv(dcfg, i, ctx_len))
-        wbytes_tok = dm.embed.nbytes + sum(sum(v.nbytes for v in L.values() if v is not None) for L in dm.layers)
+        wbytes_tok = dm.embed.nbytes + sum(sum(v.nbytes for v in L.values() if isinstance(v, np.ndarray))
+                                           for L in dm.layers)
         del dm
         def time_tokens(run, stream, n):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

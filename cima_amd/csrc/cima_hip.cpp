@@ -795,25 +795,51 @@ int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
     const int head_type = d->head ? d->head_type : d->embed_type;
     // enqueue_decode_device (src/models/transformer.rs:1440-1461)
     if (int rc = cima_hip_gguf_gather(ctx, d->embed_type, d->embed, d->ids, d->x, 1, d->hidden)) return rc;
+    auto ty = [&](int t) { return t ? t : d->ggml_type; };
     for (int l = 0; l < d->n_layers; l++) {
         const cima_decoder_layer& L = d->layers[l];
-        // rmsnorm -> q|k|v GEMV with bias (forward_chunk_at :1030-1098)
-        if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.attn_norm, d->rms_eps, L.wqkv, L.bqkv,
-                                                d->qkv, qd + 2 * kvd, d->hidden, 0, CIMA_DT_F16))
-            return rc;
+        if ((L.wk == nullptr) != (L.wv == nullptr))
+            return fail(CIMA_E_INVALID, "%s: layer %d sets one of wk / wv", api, l);
+        if (L.w_up && ty(L.type_gate) != ty(L.type_up))
+            return fail(CIMA_E_INVALID, "%s: layer %d: gate and up formats differ (%d, %d)", api, l,
+                        ty(L.type_gate), ty(L.type_up));
+        // rmsnorm -> q|k|v GEMV with bias (forward_chunk_at :1030-1098):
+        // one launch over the fused matrix, or one per projection into its
+        // slice of qkv
+        if (!L.wk) {
+            if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, ty(L.type_q), d->x, L.attn_norm, d->rms_eps, L.wqkv, L.bqkv,
+                                                    d->qkv, qd + 2 * kvd, d->hidden, 0, CIMA_DT_F16))
+                return rc;
+        } else {
+            const void* w3[3] = {L.wqkv, L.wk, L.wv};
+            const int t3[3] = {ty(L.type_q), ty(L.type_k), ty(L.type_v)};
+            const int n3[3] = {qd, kvd, kvd}, o3[3] = {0, qd, qd + kvd};
+            for (int j = 0; j < 3; j++) {
+                const void* b = L.bqkv ? static_cast<const uint16_t*>(L.bqkv) + o3[j] : nullptr;
+                if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, t3[j], d->x, L.attn_norm, d->rms_eps, w3[j], b,
+                                                        static_cast<uint16_t*>(d->qkv) + o3[j], n3[j], d->hidden, 0,
+                                                        CIMA_DT_F16))
+                    return rc;
+            }
+        }
         // rope q, k; kv append; split attention (:1100-1160)
         if (int rc = attn_fused(ctx, d->qkv, L.k_cache, L.v_cache, d->part, d->q_heads, d->kv_heads, hd, d->max_seq,
                                 csz, nch, d->rope_theta, scale, d->pos, api))
             return rc;
         // merge of the partials -> o projection + residual (:1161-1238)
-        if (int rc = cima_hip_attn_gguf_gemv(ctx, d->ggml_type, d->part, d->q_heads, hd, csz, nch, d->max_seq, d->pos,
+        if (int rc = cima_hip_attn_gguf_gemv(ctx, ty(L.type_o), d->part, d->q_heads, hd, csz, nch, d->max_seq, d->pos,
                                              L.wo, nullptr, d->x, d->hidden, 1))
             return rc;
         // rmsnorm -> gate|up SwiGLU -> down + residual (:1240-1260)
-        if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, d->ggml_type, d->x, L.ffn_norm, d->rms_eps, L.w_gate_up,
-                                                nullptr, d->act, d->ffn, d->hidden, 2, CIMA_DT_F16))
+        if (!L.w_up) {
+            if (int rc = cima_hip_rmsnorm_gguf_gemv(ctx, ty(L.type_gate), d->x, L.ffn_norm, d->rms_eps, L.w_gate_up,
+                                                    nullptr, d->act, d->ffn, d->hidden, 2, CIMA_DT_F16))
+                return rc;
+        } else if (int rc = gemv_common(ctx, ty(L.type_gate), d->x, L.w_gate_up, L.w_up, nullptr, nullptr, d->act,
+                                        d->ffn, d->hidden, 2, CIMA_DT_F16, true, api, L.ffn_norm, d->rms_eps)) {
             return rc;
-        if (int rc = cima_hip_gguf_gemv(ctx, d->ggml_type, d->act, L.w_down, nullptr, d->x, d->hidden, d->ffn, 1,
+        }
+        if (int rc = cima_hip_gguf_gemv(ctx, ty(L.type_down), d->act, L.w_down, nullptr, d->x, d->hidden, d->ffn, 1,
                                         CIMA_DT_F16))
             return rc;
     }

@@ -45,41 +45,75 @@ class DecoderConfig:
     attn_chunk: int = 256
 
 
+# the projections of a layer, as named in a layer's "types" dict
+PROJECTIONS = ("q", "k", "v", "o", "gate", "up", "down")
+
+
 @dataclass
 class HostModel:
-    """The synthetic model on the host (packed GGUF bytes and f16 arrays)."""
+    """A model on the host (packed GGUF bytes and f16 arrays).
+
+    Each layer dict holds attn_norm, wqkv, bqkv, wo, ffn_norm, w_gate_up,
+    w_down and a "types" dict (ggml type per projection).  q, k and v are
+    one fused [q + 2 kv, hidden] matrix in wqkv when they share a format;
+    otherwise wqkv is q alone and "wk" / "wv" hold k and v.  gate and up
+    (one format) are one fused [2 ffn, hidden] matrix."""
     cfg: DecoderConfig
     embed: np.ndarray
     final_norm: np.ndarray
     layers: list = field(default_factory=list)
     head: np.ndarray | None = None
+    embed_type: int | None = None
+    head_type: int | None = None
+
+    def __post_init__(self):
+        if self.embed_type is None:
+            self.embed_type = int(self.cfg.ggml_type)
+        if self.head_type is None:
+            self.head_type = self.embed_type
 
 
 def _f16(seed: int, sigma: float, n: int, mean: float = 0.0) -> np.ndarray:
     return (synth.normal(seed, sigma, n) + np.float32(mean)).astype(np.float16)
 
 
-def synthetic_model(cfg: DecoderConfig, seed: int = 5, sigma: float = 0.02) -> HostModel:
-    """Seeded random-init weights of the configured shape; every matrix is
-    quantised to cfg.ggml_type (the tied embedding/head too)."""
+def synthetic_model(cfg: DecoderConfig, seed: int = 5, sigma: float = 0.02,
+                    tensor_types: dict | None = None) -> HostModel:
+    """Seeded random-init weights of the configured shape, every matrix
+    quantised to cfg.ggml_type (the tied embedding/head too) unless
+    ``tensor_types`` names another format for a projection ("q" ... "down",
+    as in PROJECTIONS; gate and up must agree) or for "embed" / "head"."""
     t = int(cfg.ggml_type)
+    tt = {k: int(v) for k, v in (tensor_types or {}).items()}
+    types = {p: tt.get(p, t) for p in PROJECTIONS}
+    if types["gate"] != types["up"]:
+        raise ValueError("gate and up projections must share a format")
     qd, kvd = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
     s = seed * 1000
-    embed = synth.weights(t, s + 1, sigma, cfg.vocab, cfg.hidden)
-    m = HostModel(cfg, embed, _f16(s + 2, 0.1, cfg.hidden, 1.0))
+    et = tt.get("embed", t)
+    embed = synth.weights(et, s + 1, sigma, cfg.vocab, cfg.hidden)
+    m = HostModel(cfg, embed, _f16(s + 2, 0.1, cfg.hidden, 1.0), embed_type=et)
     if not cfg.tied:
-        m.head = synth.weights(t, s + 3, sigma, cfg.vocab, cfg.hidden)
+        m.head_type = tt.get("head", t)
+        m.head = synth.weights(m.head_type, s + 3, sigma, cfg.vocab, cfg.hidden)
     for i in range(cfg.n_layers):
         b = s + 100 * (i + 1)
-        m.layers.append({
+        L = {
             "attn_norm": _f16(b + 1, 0.1, cfg.hidden, 1.0),
-            "wqkv": synth.weights(t, b + 2, sigma, qd + 2 * kvd, cfg.hidden),
             "bqkv": _f16(b + 3, 0.1, qd + 2 * kvd) if cfg.qkv_bias else None,
-            "wo": synth.weights(t, b + 4, sigma, cfg.hidden, qd),
+            "wo": synth.weights(types["o"], b + 4, sigma, cfg.hidden, qd),
             "ffn_norm": _f16(b + 5, 0.1, cfg.hidden, 1.0),
-            "w_gate_up": synth.weights(t, b + 6, sigma, 2 * cfg.ffn, cfg.hidden),
-            "w_down": synth.weights(t, b + 7, sigma, cfg.hidden, cfg.ffn),
-        })
+            "w_gate_up": synth.weights(types["gate"], b + 6, sigma, 2 * cfg.ffn, cfg.hidden),
+            "w_down": synth.weights(types["down"], b + 7, sigma, cfg.hidden, cfg.ffn),
+            "types": dict(types),
+        }
+        if types["q"] == types["k"] == types["v"]:
+            L["wqkv"] = synth.weights(types["q"], b + 2, sigma, qd + 2 * kvd, cfg.hidden)
+        else:
+            L["wqkv"] = synth.weights(types["q"], b + 2, sigma, qd, cfg.hidden)
+            L["wk"] = synth.weights(types["k"], b + 8, sigma, kvd, cfg.hidden)
+            L["wv"] = synth.weights(types["v"], b + 9, sigma, kvd, cfg.hidden)
+        m.layers.append(L)
     return m
 
 
@@ -105,15 +139,19 @@ class DeviceDecoder:
         self.cfg = c = model.cfg
         self.torch = torch
         dev = torch.device(device)
-        up = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+        # contiguous and writable (weights read from a GGUF map are views
+        # of a read-only mapping, which torch will not wrap)
+        up = lambda a: torch.from_numpy(np.require(a, requirements=["C", "W"])).to(dev)  # noqa: E731
         self._keep = []
         qd, kvd = c.q_heads * c.head_dim, c.kv_heads * c.head_dim
         self.embed = up(model.embed)
         self.head = None if model.head is None else up(model.head)
+        self.embed_type, self.head_type = int(model.embed_type), int(model.head_type)
         self.final_norm = up(model.final_norm)
         self.layers = []
         for L in model.layers:
-            d = {k: (None if v is None else up(v)) for k, v in L.items()}
+            d = {k: (None if v is None else up(v)) for k, v in L.items() if k != "types"}
+            d["types"] = dict(L.get("types") or {})
             d["k_cache"] = torch.zeros((c.kv_heads, c.max_seq, c.head_dim), dtype=torch.float16, device=dev)
             d["v_cache"] = torch.zeros_like(d["k_cache"])
             self.layers.append(d)
@@ -135,12 +173,16 @@ class DeviceDecoder:
         p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         arr = (DecoderLayer * c.n_layers)()
         for i, L in enumerate(self.layers):
+            ty = L["types"]
             arr[i] = DecoderLayer(p(L["attn_norm"]), p(L["wqkv"]), p(L.get("bqkv")), p(L["wo"]), p(L["ffn_norm"]),
-                                  p(L["w_gate_up"]), p(L["w_down"]), p(L["k_cache"]), p(L["v_cache"]))
+                                  p(L["w_gate_up"]), p(L["w_down"]), p(L["k_cache"]), p(L["v_cache"]),
+                                  p(L.get("wk")), p(L.get("wv")), None,
+                                  *[int(ty.get(n, 0)) for n in PROJECTIONS])
         self._keep.append(arr)
         t = int(c.ggml_type)
         return Decoder(
-            ggml_type=t, embed_type=t, head_type=t, n_layers=c.n_layers, hidden=c.hidden, q_heads=c.q_heads,
+            ggml_type=t, embed_type=self.embed_type, head_type=self.head_type, n_layers=c.n_layers,
+            hidden=c.hidden, q_heads=c.q_heads,
             kv_heads=c.kv_heads, head_dim=c.head_dim, ffn=c.ffn, vocab=c.vocab, max_seq=c.max_seq,
             attn_chunk=c.attn_chunk, rope_theta=c.rope_theta, rms_eps=c.rms_eps, embed=p(self.embed),
             head=p(self.head), final_norm=p(self.final_norm),

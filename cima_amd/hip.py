@@ -47,8 +47,10 @@ EXPORTS = (
 
 class DecoderLayer(ctypes.Structure):
     """``cima_decoder_layer`` (include/cima_hip.h)."""
-    _fields_ = [(n, ctypes.c_void_p) for n in (
-        "attn_norm", "wqkv", "bqkv", "wo", "ffn_norm", "w_gate_up", "w_down", "k_cache", "v_cache")]
+    _fields_ = ([(n, ctypes.c_void_p) for n in (
+        "attn_norm", "wqkv", "bqkv", "wo", "ffn_norm", "w_gate_up", "w_down", "k_cache", "v_cache", "wk", "wv",
+        "w_up")]
+        + [(n, ctypes.c_int) for n in ("type_q", "type_k", "type_v", "type_o", "type_gate", "type_up", "type_down")])
 
 
 class Decoder(ctypes.Structure):

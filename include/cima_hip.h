@@ -249,6 +249,16 @@ typedef struct cima_decoder_layer {
     const void* w_down;     /* [hidden, ffn] */
     void* k_cache;          /* f16 [kv_heads, max_seq, head_dim] */
     void* v_cache;          /* f16 [kv_heads, max_seq, head_dim] */
+    /* Per-tensor formats, as GGUF files mix them (a Q4_K_M file keeps some
+     * v and down projections in Q6_K, 896-wide rows in Q5_0 / Q8_0):
+     * 0 = the decoder's ggml_type.  With wk and wv set, wqkv is the q
+     * projection alone and k, v are separate matrices (type_q / type_k /
+     * type_v); with w_up set, w_gate_up is the gate projection alone
+     * (type_gate must equal type_up). */
+    const void* wk;         /* [kv_heads * head_dim, hidden], or NULL */
+    const void* wv;         /* [kv_heads * head_dim, hidden], or NULL */
+    const void* w_up;       /* [ffn, hidden], or NULL */
+    int type_q, type_k, type_v, type_o, type_gate, type_up, type_down;
 } cima_decoder_layer;
 
 /* A decoder and its device workspace for cima_hip_decode_step. */
@@ -282,7 +292,7 @@ typedef struct cima_decoder {
  * pos += 1.  Replaces
  * enqueue_decode_device (src/models/transformer.rs:1440-1461) and
  * forward_chunk_at's rows == 1 path (:1012-1300): 5 launches per layer
- * where the reference issues about 12. */
+ * where the reference issues about 12 (7 with separate q, k, v matrices). */
 int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d);
 
 /* ---------------------------------------------------------------------

@@ -168,10 +168,12 @@ def decode_step(m: dict, token: int, pos: int, threads: int = 8):
     """One greedy decode step of a Qwen2-shaped model held in numpy.
 
     ``m``: cfg (dict with hidden, q_heads, kv_heads, head_dim, ffn, vocab,
-    rope_theta, rms_eps, type, embed_type), embed (packed [vocab, row]),
-    final_norm (f16), layers (list of dicts: attn_norm, wqkv, bqkv, wo,
-    ffn_norm, w_gate_up, w_down packed/f16, k_cache, v_cache f16 arrays
-    [kv_heads, max_seq, dim], modified in place).  The f16 roundings sit
+    rope_theta, rms_eps, type, embed_type, head_type), embed (packed [vocab,
+    row]), final_norm (f16), layers (list of dicts: attn_norm, wqkv, bqkv,
+    wo, ffn_norm, w_gate_up, w_down packed/f16, optional types (format per
+    projection, default cfg type) and wk / wv (separate k and v; wqkv is then
+    q alone), k_cache, v_cache f16 arrays [kv_heads, max_seq, dim], modified
+    in place).  The f16 roundings sit
     where the reference writes f16 activations: the gathered x, the normed
     h, q/k/v after the bias add (rounded twice: GEMV output, then bias),
     q/k after RoPE, the attention output, x after each residual add, the
@@ -186,8 +188,14 @@ def decode_step(m: dict, token: int, pos: int, threads: int = 8):
     x = gather(c["embed_type"], m["embed"], np.array([token], np.uint32), hid).view(np.float16)[0]
     scale = 1.0 / np.sqrt(hd)
     for L in m["layers"]:
+        ty = {p: (L.get("types") or {}).get(p) or t for p in ("q", "k", "v", "o", "gate", "up", "down")}
         h = rmsnorm(x, L["attn_norm"], eps)[0]
-        qkv = f16(_gemv(t, L["wqkv"], h, qd + 2 * kvd, hid, threads))
+        if L.get("wk") is None:
+            qkv = f16(_gemv(ty["q"], L["wqkv"], h, qd + 2 * kvd, hid, threads))
+        else:  # separate q, k, v matrices (formats of their own)
+            qkv = f16(np.concatenate([_gemv(ty["q"], L["wqkv"], h, qd, hid, threads),
+                                      _gemv(ty["k"], L["wk"], h, kvd, hid, threads),
+                                      _gemv(ty["v"], L["wv"], h, kvd, hid, threads)]))
         if L.get("bqkv") is not None:
             qkv = f16(qkv.astype(np.float64) + L["bqkv"].astype(np.float64))
         q = rope(qkv[:qd].reshape(1, qh, hd), pos, c["rope_theta"])[0]
@@ -195,12 +203,12 @@ def decode_step(m: dict, token: int, pos: int, threads: int = 8):
         v = qkv[qd + kvd:].reshape(1, kvh, hd)
         kv_append(L["k_cache"], L["v_cache"], k, v, pos)
         att = f16(attention(q, L["k_cache"], L["v_cache"], pos + 1, scale)).reshape(-1)
-        x = f16(x.astype(np.float64) + _gemv(t, L["wo"], att, hid, qd, threads))
+        x = f16(x.astype(np.float64) + _gemv(ty["o"], L["wo"], att, hid, qd, threads))
         h = rmsnorm(x, L["ffn_norm"], eps)[0]
-        gu = _gemv(t, L["w_gate_up"], h, 2 * ffn, hid, threads)
+        gu = _gemv(ty["gate"], L["w_gate_up"], h, 2 * ffn, hid, threads)
         g, u = f16(gu[:ffn]).astype(np.float64), f16(gu[ffn:]).astype(np.float64)
         act = f16(g / (1.0 + np.exp(-g)) * u)
-        x = f16(x.astype(np.float64) + _gemv(t, L["w_down"], act, hid, ffn, threads))
+        x = f16(x.astype(np.float64) + _gemv(ty["down"], L["w_down"], act, hid, ffn, threads))
     h = rmsnorm(x, m["final_norm"], eps)[0]
     head = m.get("head")
     ht = c.get("head_type", c["embed_type"]) if head is not None else c["embed_type"]

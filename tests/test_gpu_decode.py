@@ -293,7 +293,7 @@ def _oracle_model(m, kvs):
     c = m.cfg
     return dict(cfg=dict(hidden=c.hidden, q_heads=c.q_heads, kv_heads=c.kv_heads, head_dim=c.head_dim, ffn=c.ffn,
                          vocab=c.vocab, rope_theta=c.rope_theta, rms_eps=c.rms_eps, type=int(c.ggml_type),
-                         embed_type=int(c.ggml_type)),
+                         embed_type=int(m.embed_type), head_type=int(m.head_type)),
                 embed=m.embed, head=m.head, final_norm=m.final_norm,
                 layers=[dict(L, k_cache=kv[0].copy(), v_cache=kv[1].copy()) for L, kv in zip(m.layers, kvs)])
 
@@ -378,3 +378,39 @@ def test_decode_step_rejects_bad_descriptors(hip):
     d.desc.x = None
     with pytest.raises(EngineError):
         hip.decode_step(d.desc)
+
+
+def test_decode_step_mixed_formats_from_gguf(hip, tmp_path):
+    """A model whose tensors mix formats as GGUF files do (separate q / k /
+    v in their own formats, Q6_K v and down, Q5_0 o, Q4_K gate|up and head),
+    written to a GGUF file and loaded back: decode steps against the
+    oracle, and a graph replay identical to the eager steps."""
+    from cima_amd import gguf_file as gf
+
+    cfg = DecoderConfig(n_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                        max_seq=512, tied=False)
+    src = synthetic_model(cfg, seed=11, tensor_types={"v": 14, "down": 14, "o": 6, "gate": 12, "up": 12,
+                                                      "head": 12})
+    path = str(tmp_path / "mixed.gguf")
+    gf.save_model(path, src)
+    g = gf.GGUFFile(path)
+    m = gf.load_model(g)
+    assert "wk" in m.layers[0] and m.head_type == 12
+    kvs = [synthetic_kv(m.cfg, i, 200) for i in range(m.cfg.n_layers)]
+    d, gd = DeviceDecoder(hip, m), DeviceDecoder(hip, m)
+    for dd in (d, gd):
+        for i, (kc, vc) in enumerate(kvs):
+            dd.load_kv(i, kc, vc)
+        dd.set_state(33, 200)
+    gd.capture()
+    om = _oracle_model(m, kvs)
+    tok, pos = 33, 200
+    for s in range(3):
+        d.step()
+        gd.replay()
+        torch.cuda.synchronize()
+        ref_logits, ref_tok = od.decode_step(om, tok, pos)
+        _check_step(host(d.logits), d.token(), ref_logits, ref_tok, 1e-2)
+        assert np.all(host(d.logits) == host(gd.logits)) and d.token() == gd.token()
+        tok, pos = d.token(), pos + 1
+    g.close()
