@@ -15,8 +15,8 @@ Weights are seeded synthetic N(0, 0.02) quantised to Q4_K; x ~ N(0, 1).
 value = algorithmic bytes per step (packed weights + fp32 x and y) x steps /
 time, in GB/s.  Per-shape us/call (cold, graph-batched) for configs 1-3 are
 reported under "shapes" (with the plain streaming-read time of the same
-weight bytes, the best any kernel reads them here, and Q8_0 at the same
-Llama-3-8B shapes); "roofline" is for the fused gate+up kernel, the
+weight bytes, the best any kernel reads them here, and Q8_0 and
+bitsandbytes NF4 at the same Llama-3-8B shapes); "roofline" is for the fused gate+up kernel, the
 largest share of a step, timed with HIP events on its launch stream;
 "cpu_baseline" runs the CPU restatement of the reference's host path
 (decode to f16, fp32 dot) on a bounded sample of the same step, single
@@ -74,7 +74,7 @@ def main():
     if not cbuild.built():
         cbuild.build()
     import torch
-    from cima_amd import synth
+    from cima_amd import nf4, synth
     from cima_amd.hip import HipCtx
 
     if not torch.cuda.is_available():
@@ -211,6 +211,30 @@ def main():
                            ("q8_0 4096x4096 (q/o)", (HID, HID))]:
             shape_leg(nm, Q8_0, n, k)
         shape_leg("q8_0 4864x896 (config 1)", Q8_0, 4864, 896)
+
+        # bitsandbytes NF4 (blocksize 64, folded f32 absmax, f16 x / y) at the same shapes
+        def nf4_leg(name, n, k, bs=64, copies_mb=600):
+            g = torch.Generator(device=dev)
+            g.manual_seed(n + k)
+            nb = n * k // 2 + n * k // bs * 4  # packed nibbles + absmax, one buffer
+            ncopy = max(2, int(np.ceil(copies_mb * 1e6 / nb)))
+            bufs = []
+            for _ in range(ncopy):
+                b = torch.randint(0, 256, (nb,), dtype=torch.uint8, device=dev, generator=g)
+                b[n * k // 2:].view(torch.float32).uniform_(0.01, 0.05, generator=g)
+                bufs.append(b)
+            qm = torch.from_numpy(nf4.NF4_CODE).to(dev)
+            xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev).half()
+            ys = torch.empty(n, device=dev, dtype=torch.float16)
+            calls = max(16, min(64, 2 * ncopy))
+            us = time_calls(lambda b: ctx.nf4_gemv(xs, b, b[n * k // 2:].view(torch.float32), qm, ys, n, k, bs),
+                            bufs, calls=calls)
+            per_shape[name] = (us, nb + 2 * (n + k))
+            read_us[name] = time_calls(lambda b: ctx.stream_read(b, nb // 16 * 16, sink), bufs, calls=calls)
+        for nm, (n, k) in [("nf4 14336x4096 (gate/up)", (FFN, HID)), ("nf4 4096x14336 (down)", (HID, FFN)),
+                           ("nf4 4096x4096 (q/o)", (HID, HID))]:
+            nf4_leg(nm, n, k)
+        nf4_leg("nf4 128256x4096 (head)", 128256, HID, copies_mb=900)
         shape_leg("q6_k 128256x4096 (config 3 head)", Q6_K, 128256, HID, copies_mb=900)
         # config 4: prefill dequant-GEMM on MFMA, Q4_K 14336x4096, X bf16 (m tokens), Y fp32
         gw = synth.weights(Q4_K, 300, 0.02, FFN, HID)

@@ -5,6 +5,7 @@ Produces, in ``cima_amd/lib/``:
   cima_gemm.hsaco       prefill dequant-GEMMs (MFMA),
   cima_dequant.hsaco    dequant-to-f16 and packed gather,
   cima_decode.hsaco     decode-step support (norm, RoPE, attention, argmax)
+  cima_bnb4.hsaco       bitsandbytes NF4/FP4 dequant and decode GEMV
   libcima_hip.so      host C ABI (include/cima_hip.h), links libamdhip64
   libcima_synth.so    seeded synthetic weights + quantisers (include/cima_synth.h)
 
@@ -29,7 +30,8 @@ ARCH = "gfx950"
 # objects by format set so that they compile in parallel
 SOURCES = {"gemv_a": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=0"]), "gemv_b": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=1"]),
            "gemv_c": ("gguf_gemv.hip", ["-DCIMA_GEMV_SET=2"]), "gemm": ("gguf_gemm.hip", []),
-           "dequant": ("gguf_dequant.hip", []), "decode": ("decode_ops.hip", [])}
+           "dequant": ("gguf_dequant.hip", []), "decode": ("decode_ops.hip", []),
+           "bnb4": ("bnb4.hip", [])}
 HSACOS = {name: os.path.join(LIB, f"cima_{name}.hsaco") for name in SOURCES}
 GEMV_OBJECTS = ("gemv_a", "gemv_b", "gemv_c")
 LIBHIP = os.path.join(LIB, "libcima_hip.so")

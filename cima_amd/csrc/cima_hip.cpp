@@ -99,7 +99,7 @@ struct cima_hip_ctx {
     int device = 0;
     int num_cu = 0;
     int max_lds = 0;  // bytes of LDS one workgroup may use
-    hipModule_t modules[6] = {};  // kModuleFiles
+    hipModule_t modules[7] = {};  // kModuleFiles
     bool loaded = false;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
@@ -110,6 +110,8 @@ struct cima_hip_ctx {
     int tune_wgs = 0;  // workgroups per CU of the persistent grid (0 = built-in default)
     int tune_gemm_bn = 0;  // prefill GEMM token tile (0 = smallest built one covering m)
     int tune_ring = 0;     // GEMV main loop: 0 = heuristic, 1 = item ring where built, 2 = never
+    int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
+    int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
 };
 
 namespace {
@@ -130,9 +132,10 @@ int launch(cima_hip_ctx* ctx, hipFunction_t f, unsigned grid, unsigned block, vo
 
 // code objects: the GEMVs in three (format sets compiled in parallel),
 // the prefill GEMMs, dequant / gather, the decode-step kernels
-enum { MOD_GEMM = 3, MOD_DEQUANT = 4, MOD_DECODE = 5, NUM_MODULES = 6 };
+enum { MOD_GEMM = 3, MOD_DEQUANT = 4, MOD_DECODE = 5, MOD_BNB4 = 6, NUM_MODULES = 7 };
 const char* const kModuleFiles[NUM_MODULES] = {"cima_gemv_a.hsaco", "cima_gemv_b.hsaco", "cima_gemv_c.hsaco",
-                                               "cima_gemm.hsaco", "cima_dequant.hsaco", "cima_decode.hsaco"};
+                                               "cima_gemm.hsaco",   "cima_dequant.hsaco", "cima_decode.hsaco",
+                                               "cima_bnb4.hsaco"};
 
 // decode-step kernels (cima_decode.hsaco)
 const char* const kDecodeKernels[] = {
@@ -367,6 +370,16 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_gather_") + F->name);
     }
     if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
+    for (const char* kn : {"cima_nf4_dequant_v", "cima_nf4_dequant_e", "cima_nf4_gemv_e_f16_f16",
+                           "cima_nf4_gemv_e_f32_f32"})
+        if (!rc) rc = add(MOD_BNB4, kn);
+    for (const char* var : {"t", "c"})
+        for (int r : {1, 2, 4})
+            for (const char* a : {"f16", "f32"}) {
+                char name[64];
+                snprintf(name, sizeof name, "cima_nf4_gemv_%s_r%d_%s_%s", var, r, a, a);
+                if (!rc) rc = add(MOD_BNB4, name);
+            }
     for (const char* kn : kDecodeKernels)
         if (!rc) rc = add(MOD_DECODE, kn);
     if (rc) {
@@ -907,3 +920,104 @@ int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, u
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------ bitsandbytes 4-bit
+
+int cima_hip_set_nf4_tuning(cima_hip_ctx* ctx, int rows, int kernel) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_nf4_tuning: null context");
+    if (rows != 0 && rows != 1 && rows != 2 && rows != 4)
+        return fail(CIMA_E_INVALID, "cima_hip_set_nf4_tuning: rows %d is not 0, 1, 2 or 4", rows);
+    if (kernel < 0 || kernel > 2) return fail(CIMA_E_INVALID, "cima_hip_set_nf4_tuning: kernel %d is not 0, 1 or 2", kernel);
+    ctx->tune_nf4_rows = rows;
+    ctx->tune_nf4_kernel = kernel;
+    return 0;
+}
+
+int cima_hip_nf4_dequant(cima_hip_ctx* ctx, const void* packed, const float* absmax, const float* qmap, void* out,
+                         long long n, int blocksize) {
+    const char* api = "cima_hip_nf4_dequant";
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    if (n < 0 || blocksize <= 0) return fail(CIMA_E_INVALID, "%s: n=%lld blocksize=%d", api, n, blocksize);
+    if (n == 0) return 0;
+    if (!packed || !absmax || !qmap || !out) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    if (!aligned(absmax, 4) || !aligned(qmap, 4) || !aligned(out, 2))
+        return fail(CIMA_E_INVALID, "%s: misaligned absmax / qmap (4 B) or out (2 B)", api);
+    const void* pk = packed;
+    const float* am = absmax;
+    const float* qm = qmap;
+    void* o = out;
+    if (n % 32 == 0 && blocksize % 32 == 0 && aligned(packed, 16) && aligned(out, 16)) {
+        long long nseg = n / 32;
+        int spb = blocksize / 32;
+        long long grid = (nseg + 255) / 256;
+        if (grid > 0x7fffffffLL) return fail(CIMA_E_INVALID, "%s: n=%lld is too large", api, n);
+        void* args[] = {&pk, &am, &qm, &o, &nseg, &spb};
+        return launch_named(ctx, "cima_nf4_dequant_v", (unsigned)grid, 256, args, api);
+    }
+    long long nn = n;
+    int bs = blocksize;
+    long long grid = (n + 255) / 256;
+    if (grid > 0x7fffffffLL) return fail(CIMA_E_INVALID, "%s: n=%lld is too large", api, n);
+    void* args[] = {&pk, &am, &qm, &o, &nn, &bs};
+    return launch_named(ctx, "cima_nf4_dequant_e", (unsigned)grid, 256, args, api);
+}
+
+int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax, const float* qmap,
+                      void* y, int n, int k, int blocksize, int act_dtype) {
+    const char* api = "cima_hip_nf4_gemv";
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    if (act_dtype != CIMA_DT_F32 && act_dtype != CIMA_DT_F16)
+        return fail(CIMA_E_INVALID, "%s: act_dtype %d is not CIMA_DT_F32 or CIMA_DT_F16", api, act_dtype);
+    if (n < 0 || k <= 0 || blocksize <= 0) return fail(CIMA_E_INVALID, "%s: n=%d k=%d blocksize=%d", api, n, k, blocksize);
+    if (n == 0) return 0;
+    if (!x || !packed || !absmax || !qmap || !y) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    const int esz = act_dtype == CIMA_DT_F32 ? 4 : 2;
+    if (!aligned(x, esz) || !aligned(y, esz) || !aligned(absmax, 4) || !aligned(qmap, 4))
+        return fail(CIMA_E_INVALID, "%s: misaligned x / y (%d B) or absmax / qmap (4 B)", api, esz);
+    const char* an = act_dtype == CIMA_DT_F32 ? "f32" : "f16";
+    const void* xp = x;
+    const void* pk = packed;
+    const float* am = absmax;
+    const float* qm = qmap;
+    void* yp = y;
+    int nn = n, kk = k;
+    const bool pow2 = (blocksize & (blocksize - 1)) == 0;
+    const long long segs_total = (long long)n * (k / 32);
+    const long long tab_lds = 65536LL + 2LL * k;  // pair table + x
+    if (k % 32 == 0 && blocksize >= 32 && pow2 && aligned(packed, 16) && aligned(x, 16) && segs_total < (1LL << 32) &&
+        2LL * k <= ctx->max_lds) {
+        int bshift = 0;
+        while ((32 << bshift) < blocksize) bshift++;
+        // the pair table when it fits next to x (1024-thread workgroups, one
+        // per CU), else the codebook in registers (256-thread workgroups)
+        bool tab = tab_lds <= ctx->max_lds;
+        if (ctx->tune_nf4_kernel == 1 && !tab)
+            return fail(CIMA_E_INVALID, "%s: k=%d does not leave room for the pair table in LDS", api, k);
+        if (ctx->tune_nf4_kernel == 2) tab = false;
+        const int wpg = tab ? 16 : 4;  // waves per workgroup
+        // measured on MI355X (4096-128256 rows, k 4096 and 14336): the table
+        // kernel with one row per wave and two workgroups per CU where the
+        // LDS holds them was the fastest or within 5% of it
+        const long long wgs = ctx->tune_wgs ? ctx->tune_wgs : (!tab || 2 * tab_lds <= ctx->max_lds ? 2 : 1);
+        const long long waves = wgs * ctx->num_cu * wpg;
+        int r = ctx->tune_nf4_rows;
+        if (!r) r = tab ? 1 : ((n + 3) / 4 >= waves ? 4 : ((n + 1) / 2 >= waves ? 2 : 1));
+        const long long groups = (n + r - 1) / r;
+        long long grid = (groups + wpg - 1) / wpg;
+        if (grid > wgs * ctx->num_cu) grid = wgs * ctx->num_cu;
+        // a wave keeps the sums of its rows in one register until the end: at most 64 rows per wave
+        const long long min_waves = (groups * r + 63) / 64;
+        if (grid < (min_waves + wpg - 1) / wpg) grid = (min_waves + wpg - 1) / wpg;
+        char name[64];
+        snprintf(name, sizeof name, "cima_nf4_gemv_%s_r%d_%s_%s", tab ? "t" : "c", r, an, an);
+        hipFunction_t f;
+        if (int rc = get_fn(ctx, name, &f)) return rc;
+        void* args[] = {&xp, &pk, &am, &qm, &yp, &nn, &kk, &bshift};
+        return launch(ctx, f, (unsigned)grid, 64 * wpg, args, api, (unsigned)(tab ? tab_lds : 2LL * k));
+    }
+    int bs = blocksize;
+    char name[64];
+    snprintf(name, sizeof name, "cima_nf4_gemv_e_%s_%s", an, an);
+    void* args[] = {&xp, &pk, &am, &qm, &yp, &nn, &kk, &bs};
+    return launch_named(ctx, name, (unsigned)((n + 3) / 4), 256, args, api);
+}

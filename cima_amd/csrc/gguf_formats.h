@@ -35,6 +35,27 @@ DEV uint32_t f2h2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2_t){lo, hi}, h2_t));
 }
 
+// ------------------------------------------------------ reductions (wave64)
+
+// Sum over aligned groups of `width` lanes (16, 32 or 64); the total lands in
+// the LAST lane of each group.  Rows of 16 lanes reduce with DPP quad
+// permutes and half-row / row mirrors (every lane of the row then holds the
+// row sum); row_bcast:15 / row_bcast:31 then fold rows 0->1, 2->3 and 1->3.
+template <int CTRL, int ROW_MASK>
+DEV float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                     0xf, false));
+}
+DEV float group_sum_last(float v, int width) {
+    v = dpp_add<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xf>(v);  // row_half_mirror
+    v = dpp_add<0x140, 0xf>(v);  // row_mirror
+    if (width >= 32) v = dpp_add<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    if (width >= 64) v = dpp_add<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
 DEV uint4 ld16a(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
 // 2-byte-aligned 16-byte load: gfx950 runs with unaligned global access
 // enabled, so this is one global_load_dwordx4 (measured at full streaming

@@ -27,7 +27,7 @@ LIBHIP = os.path.join(LIB_DIR, "libcima_hip.so")
 # the gfx950 code objects cima_hip_init loads (names as cima_amd/build.py
 # writes them)
 CODE_OBJECTS = [os.path.join(LIB_DIR, f"cima_{n}.hsaco")
-                for n in ("gemv_a", "gemv_b", "gemv_c", "gemm", "dequant", "decode")]
+                for n in ("gemv_a", "gemv_b", "gemv_c", "gemm", "dequant", "decode", "bnb4")]
 
 # declared in include/cima_hip.h, in order
 EXPORTS = (
@@ -41,6 +41,7 @@ EXPORTS = (
     "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
     "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
+    "cima_hip_nf4_dequant", "cima_hip_nf4_gemv", "cima_hip_set_nf4_tuning",
     "cima_hip_stream_read",
 )
 
@@ -119,6 +120,9 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_decode_step.argtypes = [P, ctypes.POINTER(Decoder)]
     L.cima_hip_capture_begin.argtypes = [P]
     L.cima_hip_stream_read.argtypes = [P, P, LL, P]
+    L.cima_hip_nf4_dequant.argtypes = [P, P, P, P, P, LL, I]
+    L.cima_hip_nf4_gemv.argtypes = [P, P, P, P, P, P, I, I, I, I]
+    L.cima_hip_set_nf4_tuning.argtypes = [P, I, I]
     L.cima_hip_capture_end.argtypes = [P, ctypes.POINTER(P)]
     L.cima_hip_graph_launch.argtypes = [P, P]
     L.cima_hip_graph_destroy.argtypes = [P]
@@ -265,6 +269,25 @@ class HipCtx:
         """``out[i,:] = dequant(table[ids[i]])`` as f16."""
         self._check(self.lib.cima_hip_gguf_gather(self.handle, int(fmt), _ptr(table), _ptr(ids), _ptr(out),
                                                   n, hidden))
+
+    # -- bitsandbytes 4-bit (src/quant.rs:18-437) ----------------------------
+    def nf4_dequant(self, packed, absmax, qmap, out, n: int, blocksize: int) -> None:
+        """CudaCtx::nf4_dequant (src/cuda.rs:2321): ``out[i] = f16(qmap[nib(i)] * absmax[i // blocksize])``."""
+        self._check(self.lib.cima_hip_nf4_dequant(self.handle, _ptr(packed), _ptr(absmax), _ptr(qmap), _ptr(out),
+                                                  n, blocksize))
+
+    def nf4_gemv(self, x, packed, absmax, qmap, y, n: int, k: int, blocksize: int,
+                 act_dtype: Optional[int] = None) -> None:
+        """CudaCtx::nf4_gemv (src/cuda.rs:2347): ``y[n] = W[n, k] . x`` over the packed weight."""
+        if act_dtype is None:
+            act_dtype = _act_of(x) if hasattr(x, "dtype") else gguf.DT_F16
+        self._check(self.lib.cima_hip_nf4_gemv(self.handle, _ptr(x), _ptr(packed), _ptr(absmax), _ptr(qmap), _ptr(y),
+                                               n, k, blocksize, act_dtype))
+
+    def set_nf4_tuning(self, rows: int = 0, kernel: int = 0) -> None:
+        """Fast NF4 GEMV: rows per wave (1, 2, 4) and kernel (1 = LDS pair table,
+        2 = codebook in registers); 0 = heuristic."""
+        self._check(self.lib.cima_hip_set_nf4_tuning(self.handle, int(rows), int(kernel)))
 
     def rmsnorm_gguf_gemv(self, fmt: int, x, norm_w, eps: float, w, bias, y, n: int, k: int, mode: int = 0,
                           act_dtype: Optional[int] = None) -> None:

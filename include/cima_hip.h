@@ -308,6 +308,35 @@ int cima_hip_capture_end(cima_hip_ctx* ctx, cima_hip_graph** out);
 int cima_hip_graph_launch(cima_hip_ctx* ctx, cima_hip_graph* graph);
 int cima_hip_graph_destroy(cima_hip_graph* graph);
 
+/* ---------------------------------------------------------------------
+ * bitsandbytes 4-bit weights (NF4 / FP4), src/quant.rs:18-437: a
+ * row-major [n, k] weight resident as n*k/2 packed bytes (element 2j in the
+ * HIGH nibble of byte j), absmax[n*k / blocksize] f32 (the double
+ * quantisation folded on the host, src/quant.rs:258-330) and the 16-entry
+ * f32 codebook qmap.  Element i = qmap[nibble(i)] * absmax[i / blocksize].
+ * --------------------------------------------------------------------- */
+/* out[i] = f16(qmap[nibble(i)] * absmax[i / blocksize]) for i < n, bit-exact
+ * (one fp32 product rounded to nearest even).  Replaces CudaCtx::nf4_dequant
+ * (src/cuda.rs:2321-2345, k_nf4_dequant src/kernels.cu:320-329).  absmax /
+ * qmap 4-byte, out 2-byte aligned; n % 32 == 0, blocksize % 32 == 0 with
+ * 16-byte aligned packed and out take the vector kernel. */
+int cima_hip_nf4_dequant(cima_hip_ctx* ctx, const void* packed, const float* absmax, const float* qmap, void* out_f16,
+                         long long n, int blocksize);
+/* Fused decode GEMV y[n] = W[n, k] . x[k] over the packed weight.  Replaces
+ * CudaCtx::nf4_gemv (src/cuda.rs:2347-2381, k_nf4_gemv / k_nf4_gemv_ref
+ * src/kernels.cu:331-387).  act_dtype CIMA_DT_F16 (x, y f16, as the
+ * reference) or CIMA_DT_F32 (x, y fp32; x rounded to f16 inside).  Codes
+ * are used as f16 (relative error <= 2^-11 each), fp32 accumulation.
+ * k % 32 == 0, blocksize a power of two >= 32 and 16-byte aligned packed
+ * and x take the fast kernels; any other shape a general one. */
+int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax, const float* qmap,
+                      void* y, int n, int k, int blocksize, int act_dtype);
+/* Tuning of the fast NF4 GEMV (no counterpart in the reference): rows each
+ * wave walks together (0 = heuristic, 1, 2 or 4) and the kernel (0 =
+ * heuristic, 1 = LDS pair table, 2 = codebook in registers).  The grid
+ * width follows cima_hip_set_gemv_grid. */
+int cima_hip_set_nf4_tuning(cima_hip_ctx* ctx, int rows, int kernel);
+
 /* Bandwidth reference (no counterpart in the reference): reads nbytes
  * (16-byte aligned src, whole 16-byte words) once with plain streaming
  * loads; *sink is written only in an improbable case.  The HBM read rate a

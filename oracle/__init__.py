@@ -5,8 +5,8 @@ Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 path (``cima_amd``) never imports it.
 
 The arithmetic lives in ``gguf_oracle.c`` (a C restatement of the reference's
-``src/traits.rs:832-896`` f16 primitives and ``src/quant.rs:571-896`` GGUF
-decoders); this module is a thin numpy/ctypes front end over ``liboracle.so``.
+``src/traits.rs:832-896`` f16 primitives, ``src/quant.rs:571-896`` GGUF
+decoders and ``src/quant.rs:258-437`` bitsandbytes NF4/FP4 decoding); this module is a thin numpy/ctypes front end over ``liboracle.so``.
 """
 from __future__ import annotations
 
@@ -60,6 +60,8 @@ def lib():
         L.oracle_scale_min_k4.argtypes = [I, P, P, P]
         L.oracle_f16_to_f32_array.argtypes = [P, P, S]
         L.oracle_f32_to_f16_array.argtypes = [P, P, S]
+        L.oracle_nf4_fold_absmax.argtypes = [P, S, P, P, S, S, ctypes.c_float, P]
+        L.oracle_nf4_dequant.argtypes = [P, P, P, P, S, S]
         _lib = L
     return _lib
 
@@ -166,3 +168,40 @@ def scale_min_k4(j: int, scales: np.ndarray):
     sc, m = ctypes.c_float(), ctypes.c_float()
     lib().oracle_scale_min_k4(j, _p(s), ctypes.byref(sc), ctypes.byref(m))
     return sc.value, m.value
+
+
+# ------------------------------------------------------------ bitsandbytes 4-bit
+
+def nf4_fold_absmax(codes: np.ndarray, nested_quant_map: np.ndarray, nested_absmax: np.ndarray,
+                    nested_blocksize: int, nested_offset: float) -> np.ndarray:
+    """folded_absmax (src/quant.rs:258-330), double-quantised branch."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint8)
+    nmap = np.ascontiguousarray(nested_quant_map, dtype=np.float32)
+    nabs = np.ascontiguousarray(nested_absmax, dtype=np.float32)
+    if nmap.size != 256:
+        raise ValueError("nested_quant_map must have 256 entries")
+    out = np.zeros(codes.size, dtype=np.float32)
+    rc = lib().oracle_nf4_fold_absmax(_p(codes), codes.size, _p(nmap), _p(nabs), nabs.size, nested_blocksize,
+                                      float(nested_offset), _p(out))
+    if rc:
+        raise ValueError("nested_absmax too short")
+    return out
+
+
+def nf4_dequant(packed: np.ndarray, absmax: np.ndarray, qmap: np.ndarray, n: int, blocksize: int) -> np.ndarray:
+    """dequant_host (src/quant.rs:401-437): f16 bits of qmap[nib(i)] * absmax[i // blocksize]."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(-1)
+    absmax = np.ascontiguousarray(absmax, dtype=np.float32)
+    qmap = np.ascontiguousarray(qmap, dtype=np.float32)
+    if packed.size * 2 < n or absmax.size * blocksize < n or qmap.size != 16:
+        raise ValueError("nf4 operands too short")
+    out = np.zeros(n, dtype=np.uint16)
+    if lib().oracle_nf4_dequant(_p(packed), _p(absmax), _p(qmap), _p(out), n, blocksize):
+        raise ValueError("nf4_dequant: n must be even and a multiple of blocksize")
+    return out
+
+
+def nf4_gemv(packed: np.ndarray, absmax: np.ndarray, qmap: np.ndarray, x: np.ndarray, n: int, k: int,
+             blocksize: int, threads: int = 1) -> np.ndarray:
+    """The reference CPU path for a packed weight: dequant_host, then the fp32 GEMV over the f16 weights."""
+    return gemv(nf4_dequant(packed, absmax, qmap, n * k, blocksize), x, n, k, threads=threads)

@@ -23,6 +23,11 @@
  *                        to float16 (closed form: every product is exact);
  *                        committed fixtures from that decoder.
  *   storage sizes        reference test src/quant.rs:1207-1218.
+ *   nf4 dequant / fold   the reference has no NF4 test: pinned by an
+ *                        independent numpy restatement (tests/test_nf4.py,
+ *                        closed form f16(f32(code * absmax))), exact special
+ *                        cases (power-of-two codes and scales) and the
+ *                        nibble order src/kernels.cu:320-329 states.
  *   gemv / gemm          brute-force float64 dot over the decoded weights
  *                        (numpy einsum in the tests); epilogue semantics
  *                        against their closed forms.
@@ -342,6 +347,39 @@ int oracle_dequant_q6_k(const uint8_t* src, size_t src_len, size_t numel, uint16
                 out[base + l + 96] = oracle_f32_to_f16(d * (float)(int8_t)sch[is + 6] * (float)q4);
             }
         }
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* bitsandbytes NF4 / FP4 (src/quant.rs:18-437): packed nibbles (element
+ * 2j the HIGH nibble of byte j), f32 absmax per blocksize elements, a
+ * 16-entry f32 codebook */
+
+/* folded_absmax, src/quant.rs:258-330 (the double-quantised branch):
+ * absmax[i] = nested_quant_map[code[i]] * nested_absmax[i / nested_blocksize]
+ * + nested_offset, each operation rounded in f32.  -1 when nested_absmax is
+ * too short. */
+int oracle_nf4_fold_absmax(const uint8_t* codes, size_t nblocks, const float* nested_quant_map,
+                           const float* nested_absmax, size_t n_nested, size_t nested_blocksize,
+                           float nested_offset, float* out) {
+    for (size_t i = 0; i < nblocks; i++) {
+        size_t j = i / nested_blocksize;
+        if (j >= n_nested) return -1;
+        float p = nested_quant_map[codes[i]] * nested_absmax[j];
+        out[i] = p + nested_offset;
+    }
+    return 0;
+}
+
+/* dequant_host, src/quant.rs:401-437: w[i] = f16(qmap[nib(i)] * absmax[i / bs]) */
+int oracle_nf4_dequant(const uint8_t* packed, const float* absmax, const float* qmap, uint16_t* out, size_t n,
+                       size_t blocksize) {
+    if (!blocksize || n % 2 || n % blocksize) return -1;
+    for (size_t i = 0; i < n; i++) {
+        uint8_t b = packed[i / 2];
+        int nib = (i % 2 == 0) ? (b >> 4) : (b & 0x0F);
+        out[i] = oracle_f32_to_f16(qmap[nib] * absmax[i / blocksize]);
     }
     return 0;
 }

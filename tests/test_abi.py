@@ -75,6 +75,15 @@ def test_decode_object_holds_every_kernel():
         assert n.encode() in blob, n
 
 
+def test_bnb4_object_holds_every_kernel():
+    blob = open(cbuild.HSACOS["bnb4"], "rb").read()
+    names = ["cima_nf4_dequant_v", "cima_nf4_dequant_e"]
+    names += [f"cima_nf4_gemv_{v}_r{r}_{a}_{a}" for v in ("t", "c") for r in (1, 2, 4) for a in ("f16", "f32")]
+    names += [f"cima_nf4_gemv_e_{a}_{a}" for a in ("f16", "f32")]
+    for n in names:
+        assert n.encode() in blob, n
+
+
 def test_decoder_struct_layout_matches_header(tmp_path):
     """The ctypes mirrors of cima_decoder / cima_decoder_layer have the C
     layout (compiled with the header by the host compiler)."""
@@ -204,6 +213,9 @@ def test_hot_gemv_kernels_do_not_spill():
             for a in ("f32", "f16") for e in ("", "_epi")]
     hot += [f"cima_gemv_{f}_r1_i1_f16_{v}" for f in ("q8_0", "q4_k") for v in ("att_epi", "amax", "ring_amax")]
     spills = {k: notes[k] for k in hot if notes[k][1] > 0}
+    assert not spills, spills
+    notes = _kernel_notes(cbuild.HSACOS["bnb4"])
+    spills = {k: v for k, v in notes.items() if (k.startswith("cima_nf4_gemv_t") or k.startswith("cima_nf4_gemv_c")) and v[1] > 0}
     assert not spills, spills
 
 
