@@ -7,14 +7,17 @@
 // Y[m, n] (row stride ldy) = X[m, k] . W[n, k]^T: X holds m tokens, W is the
 // packed GGUF weight (the engine's lin_gemm, src/models/transformer.rs:
 // 618-655, which dequantises W to an f16 slab and runs an f16 GEMM).
-// Each stage (BM weight rows x BK k, 8192 weights), a 256-thread workgroup
-// dequantises its weights to f16 in LDS -- bit-exact with the host
-// decoders, so the operand equals the reference's dequantised weight --
-// stages the X tile as f16 (bf16 -> f16 is exact for 2^-14 <= |x| < 65520), and
-// runs v_mfma_f32_16x16x32_f16 with fp32 accumulation.  Wave w owns weight
-// rows [w BM/4, (w+1) BM/4) of the tile and all BN tokens.  LDS is
-// double-buffered; the global loads of the next PF stages are in flight in
-// registers while a stage is multiplied.
+// Each stage a 256-thread workgroup dequantises its weight tile to f16 --
+// bit-exact with the host decoders, so the operand equals the reference's
+// dequantised weight -- stages the X tile as f16 in LDS (bf16 -> f16 is
+// exact for 2^-14 <= |x| < 65520), and multiplies with f16 MFMA, fp32
+// accumulation.  Wave w owns weight rows [w BM/4, (w+1) BM/4) of the tile
+// and all BN tokens.  LDS is double-buffered; the global loads of the next
+// PF stages are in flight in registers while a stage is multiplied.  Two
+// kernels: gemm_body (16 tokens, weights through LDS, 16x16x32 MFMA),
+// gemm_body_ra (64 tokens, weights dequantised into the A operand
+// registers, 32x32x16 MFMA) and gemm_body_wide (128 tokens, weights
+// through LDS, 32x32x16 MFMA).
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -243,7 +246,9 @@ struct XTile {
             uint16_t* dst = xl + mp.lds[i];
             const uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
             if constexpr (XT == XT_F16) {
-                *reinterpret_cast<uint4*>(dst) = r[i];
+                // component-wise: a whole-struct copy here leaves the load
+                // ring in scratch memory (the aggregate is not promoted)
+                *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
             } else if constexpr (XT == XT_BF16) {
                 // bf16 -> f16 is exact for 2^-14 <= |x| < 65520
                 uint32_t o[4];
@@ -260,12 +265,18 @@ struct XTile {
     }
 };
 
-// Tile shapes.  A stage is BM weight rows x BK k (8192 weights: one
-// 32-element sub-block per thread of the 256).  BN = 16 (up to 16 tokens)
-// takes 64 rows x 128 k so a 14336-row weight spreads over 224 workgroups;
-// wider token tiles take 128 rows x 64 k.  PF stages of weights and
+// Tile shapes.  BN = 16 (up to 16 tokens): gemm_body, a stage of 64 rows x
+// 128 k (8192 weights: one 32-element sub-block per thread of the 256), so a
+// 14336-row weight spreads over 224 workgroups.  BN = 64: gemm_body_ra,
+// 128 rows (32 per wave) x 64 k per stage, weights dequantised straight
+// into the MFMA operand registers.  BN = 128: gemm_body_wide, 128 x 64
+// stages through LDS on a 2 x 2 wave grid.  PF stages of weights and
 // activations are in flight in registers, in the order they are consumed
-// (the memory counter retires loads in issue order).
+// (the memory counter retires loads in issue order).  Measured on MI355X
+// (14336x4096 Q4_K, bf16 X, the two kernels in one process): register-A
+// tiles 40 / 43 / 44 us at m = 32 / 64 / 128 against 44 / 47 / 48 us
+// through LDS; at m = 256 / 512 the LDS-staged 2 x 2 grid is faster (68 /
+// 105 us against 72 / 112).
 template <int BN> struct GemmTile;
 template <> struct GemmTile<16> { static constexpr int BM = 64, PF = 8; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
@@ -381,7 +392,9 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
     }
 }
 
-// Wide token tiles (BN = 64, 128): v_mfma_f32_32x32x16_f16 on a 2 x 2 grid
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+// Wide token tiles (BN = 128): v_mfma_f32_32x32x16_f16 on a 2 x 2 grid
 // of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
 // 128-row tile and tokens [wc BN/2, (wc+1) BN/2) -- so every A fragment
 // read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k
@@ -389,7 +402,6 @@ __device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict_
 // (measured on MI355X, 14336x4096 Q4_K: 64 tokens 52.5 -> 49.0 us from 2
 // to 4 stages, 256 tokens 83 -> 69 us from 1 to 2), and two workgroups
 // share a CU.
-typedef float float16_t __attribute__((ext_vector_type(16)));
 
 
 template <typename D, int BN, int XT, int YT>
@@ -495,12 +507,131 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
     }
 }
 
+// Register-A tiles: each wave owns RW weight rows (RW / 32 tiles of 32
+// rows) and all BN tokens of the workgroup's tile, and dequantises its own
+// A operand straight into registers -- no LDS round trip for the weights.
+// Lane l of a 32-row tile takes row l % 32 and dequantises sub-block
+// h = l / 32 of the stage's two (64 k): its 32 values are the A fragments of
+// the four k-steps, step q holding elements [8q, 8q+8).  The MFMA sums over
+// k in any order as long as A and B agree, so the B fragment of lane l, step
+// q, is x[32h + 8q, +8) of its token.  Only the activation tile goes through
+// LDS; per 64-k stage a wave issues 4 (RW/32) (BN/32) v_mfma_f32_32x32x16_f16.
+template <typename D, int BN, int RW, int PF, int XT, int YT>
+__device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
+                             int m, int n, int k, int ldy) {
+    constexpr int BM = 4 * RW, BK = 64, KP = BK + 8;
+    constexpr int RA = RW / 32, TB = BN / 32;
+    __shared__ __align__(16) uint16_t xl[2][BN * KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r0 = blockIdx.x * BM + RW * wave, t0 = blockIdx.y * BN;
+    const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const int nk = k / BK;
+    const int h = lane >> 5;
+
+    const uint8_t* wp[RA];
+#pragma unroll
+    for (int a = 0; a < RA; a++) wp[a] = w + (size_t)min(r0 + 32 * a + (lane & 31), n - 1) * row_bytes;
+    using XS = XTile<XT, BN, BK>;
+    const typename XS::Map xm = XS::map(t0, m, k, KP);
+    struct Stage {
+        typename D::Raw wr[RA];
+        XS xr;
+    };
+    auto issue = [&](Stage& st, int s) {
+        const int sc = min(s, nk - 1);  // stages past the end re-load the last one
+#pragma unroll
+        for (int a = 0; a < RA; a++) st.wr[a] = D::load(wp[a], 2 * sc + h);
+        st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
+    };
+
+    float16_t acc[RA][TB];
+#pragma unroll
+    for (int a = 0; a < RA; a++)
+#pragma unroll
+        for (int b = 0; b < TB; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
+
+    Stage ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) issue(ring[i], i);
+
+    auto step = [&](Stage& st, int s, bool next) {
+        const int buf = s & 1;
+        st.xr.store(xl[buf], xm);
+        uint32_t o[RA][16];
+#pragma unroll
+        for (int a = 0; a < RA; a++) D::deq(st.wr[a], 2 * s + h, o[a]);
+        __syncthreads();
+        if (next) issue(st, s + PF);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            half8_t av[RA], bv[TB];
+#pragma unroll
+            for (int a = 0; a < RA; a++)
+                av[a] = __builtin_bit_cast(half8_t, make_uint4(o[a][4 * q], o[a][4 * q + 1], o[a][4 * q + 2],
+                                                               o[a][4 * q + 3]));
+#pragma unroll
+            for (int b = 0; b < TB; b++)
+                bv[b] = *reinterpret_cast<const half8_t*>(&xl[buf][(32 * b + (lane & 31)) * KP + 32 * h + 8 * q]);
+#pragma unroll
+            for (int a = 0; a < RA; a++)
+#pragma unroll
+                for (int b = 0; b < TB; b++)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
+        }
+    };
+    int base = 0;
+    for (; base + PF <= nk; base += PF) {
+#pragma unroll
+        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
+    }
+#pragma unroll
+    for (int b0 = 0; b0 < PF - 1; b0++)
+        if (base + b0 < nk) step(ring[b0], base + b0, false);
+
+    // lane l, element i of a 32x32 tile: row 8(i/4) + 4(l/32) + i%4, column l%32
+#pragma unroll
+    for (int a = 0; a < RA; a++) {
+#pragma unroll
+        for (int b = 0; b < TB; b++) {
+            const int tok = t0 + 32 * b + (lane & 31);
+            if (tok >= m) continue;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int row = r0 + 32 * a + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                if (row < n) {
+                    const size_t off = (size_t)tok * ldy + row;
+                    if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = acc[a][b][i];
+                    else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(acc[a][b][i]);
+                }
+            }
+        }
+    }
+}
+
+// Stages in flight for gemm_body_ra: GemmTile<BN>::PF, fewer where a stage
+// (the raw weight sub-block plus the thread's activation words) is so large
+// that the ring would spill to scratch memory.
+template <typename D, int BN, int XT>
+constexpr int ra_pf() {
+    if constexpr (BN < 32) {
+        return 1;  // not a register-A tile
+    } else {
+        constexpr int stage = (int)(sizeof(typename D::Raw) / 4) + 4 * XTile<XT, BN, 64>::NL;
+        constexpr int fit = (BN == 64 ? 84 : 60) / stage;
+        return fit < 1 ? 1 : (fit < GemmTile<BN>::PF ? fit : GemmTile<BN>::PF);
+    }
+}
+
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
     extern "C" __global__ __launch_bounds__(256, BN == 16 ? 1 : 2) void                             \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                   \
+        else if constexpr (BN == 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
         else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
     }
 #define GEMM_XY(FN, D, BN)                                                    \

@@ -223,3 +223,13 @@ def test_python_binding_checks_every_code_object():
     """HipCtx refuses to start without any of the code objects the build
     writes (the list the C library loads)."""
     assert sorted(hipmod.CODE_OBJECTS) == sorted(cbuild.HSACOS.values())
+
+
+def test_gemm_kernels_do_not_spill():
+    """Every prefill GEMM variant keeps its load ring in registers (a ring
+    left in scratch memory -- register pressure, or an aggregate copy the
+    compiler does not promote -- turns each stage into scratch traffic)."""
+    notes = _kernel_notes(cbuild.HSACOS["gemm"])
+    assert len(notes) == 9 * 3 * 6
+    spills = {k: v for k, v in notes.items() if v[1] > 0}
+    assert not spills, spills
