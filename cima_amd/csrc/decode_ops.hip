@@ -118,19 +118,20 @@ extern "C" __global__ __launch_bounds__(256) void cima_kv_append_f16(const uint1
 // one query head.  Every load of the chunk is issued before any of them is
 // used -- thread t's key row (position s0 + t) and a 1/256 slice of the
 // chunk's value rows -- so a chunk costs one memory round trip even when
-// the cache is cold in HBM; the values go through LDS to the weighted sum.
+// the cache is cold in HBM; the weighted value sum runs on the slices in
+// registers and reduces across lanes, with no sequential loop over the
+// chunk's positions.
 
 constexpr int ATT_MAX_CSZ = 256;
 
 template <int D>
 struct AttnLds {
-    uint16_t v[ATT_MAX_CSZ * D];  // the chunk's value rows (f16)
     float q[D];
     float kn[D];
     float vn[D];
     float p[ATT_MAX_CSZ];
     float red[8];
-    float acc[512 / D][D];  // one accumulator row per position group
+    float acc[4][D];  // one accumulator row per wave
 };
 
 // The chunk's loads, held in registers until used: thread t's key row
@@ -163,9 +164,6 @@ DEV void attn_chunk(AttnLds<D>& L, const AttnRegs<D>& R, int s0, int s1, int sne
                     float* __restrict__ dst) {
     constexpr int RV = D / 8;
     const int t = threadIdx.x, len = s1 - s0;
-    // values -> LDS (slots past the chunk take clamped copies, never read)
-#pragma unroll
-    for (int j = 0; j < RV; j++) reinterpret_cast<uint4*>(L.v)[t + 256 * j] = R.v[j];
     // score of position s0 + t
     float d = 0.f;
     if (s0 + t == snew) {
@@ -187,35 +185,47 @@ DEV void attn_chunk(AttnLds<D>& L, const AttnRegs<D>& R, int s0, int s1, int sne
     const float mw = wave_max(sc);
     if ((t & 63) == 0) L.red[t >> 6] = mw;
     __syncthreads();
-    // the new position's value row replaces what the cache held there
-    const int rnew = snew - s0;
-    if (rnew >= 0 && rnew < len && t < D) L.v[rnew * D + t] = (uint16_t)f2h(L.vn[t]);
     const float M = fmaxf(fmaxf(L.red[0], L.red[1]), fmaxf(L.red[2], L.red[3]));
     const float e = live ? __expf(sc - M) : 0.f;
     L.p[t] = e;
     const float lw = wave_sum(e);
     if ((t & 63) == 0) L.red[4 + (t >> 6)] = lw;
     __syncthreads();
-    // weighted value sum: lane pair dp owns dims 2dp, 2dp+1; G groups
-    // stride the positions
-    constexpr int G = 512 / D;
-    const int dp = t % (D / 2), g = t / (D / 2);
-    float a0 = 0.f, a1 = 0.f;
-    for (int j = g; j < len; j += G) {
-        const float pj = L.p[j];
-        const uint32_t u = reinterpret_cast<const uint32_t*>(L.v + j * D)[dp];
-        a0 += pj * h2f(u & 0xffffu);
-        a1 += pj * h2f(u >> 16);
-    }
-    L.acc[g][2 * dp] = a0;
-    L.acc[g][2 * dp + 1] = a1;
-    __syncthreads();
-    if (t < D) {
-        float a = 0.f;
+    // weighted value sum from the registers: thread t holds dims
+    // [8 (t % RV), +8) of rows t / RV + (256 / RV) j; rows past the chunk
+    // have p = 0, and the new position's row comes from L.vn
+    const int pc = t % RV, rnew = snew - s0;
+    float a[8];
 #pragma unroll
-        for (int gg = 0; gg < G; gg++) a += L.acc[gg][t];
-        dst[2 + t] = a;
+    for (int i = 0; i < 8; i++) a[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < RV; j++) {
+        const int row = t / RV + (256 / RV) * j;
+        const float pr = L.p[row];
+        const uint32_t w[4] = {R.v[j].x, R.v[j].y, R.v[j].z, R.v[j].w};
+        if (row == rnew) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) a[i] += pr * L.vn[8 * pc + i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                a[2 * i] += pr * h2f(w[i] & 0xffffu);
+                a[2 * i + 1] += pr * h2f(w[i] >> 16);
+            }
+        }
     }
+    // sum over the lanes of a wave holding the same dims (lane % RV), then
+    // over the four waves
+#pragma unroll
+    for (int o = RV; o < 64; o <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; i++) a[i] += __shfl_xor(a[i], o);
+    if ((t & 63) < RV) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) L.acc[t >> 6][8 * pc + i] = a[i];
+    }
+    __syncthreads();
+    if (t < D) dst[2 + t] = (L.acc[0][t] + L.acc[1][t]) + (L.acc[2][t] + L.acc[3][t]);
     if (t == 0) {
         dst[0] = M;
         dst[1] = (L.red[4] + L.red[5]) + (L.red[6] + L.red[7]);
