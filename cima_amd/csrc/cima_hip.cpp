@@ -188,7 +188,7 @@ struct GemvPlan {
     bool ring;       // item-ring main loop (_ring kernels)
 };
 
-// matches xstage_bytes() in gguf_kernels.hip
+// matches xstage_bytes() in gguf_gemv.hip
 size_t gemv_lds_bytes(const Fmt* F, int k) {
     size_t kk = (size_t)k;
     return 2 * kk + 16 * (kk >> F->pad_shift) + 4 * (kk >> 5) + 4 * (kk >> 4);
