@@ -7,20 +7,20 @@
 // Y[m, n] (row stride ldy) = X[m, k] . W[n, k]^T: X holds m tokens, W is the
 // packed GGUF weight (the engine's lin_gemm, src/models/transformer.rs:
 // 618-655, which dequantises W to an f16 slab and runs an f16 GEMM).
-// Each stage a 256-thread workgroup dequantises its weight tile to f16 --
-// bit-exact with the host decoders, so the operand equals the reference's
+// Each stage a workgroup dequantises its weight tile to f16 -- bit-exact
+// with the host decoders, so the operand equals the reference's
 // dequantised weight -- stages the X tile as f16 in LDS (bf16 -> f16 is
 // exact for 2^-14 <= |x| < 65520), and multiplies with f16 MFMA, fp32
-// accumulation.  Wave w owns weight rows [w BM/4, (w+1) BM/4) of the tile
-// and all BN tokens.  LDS is double-buffered; the global loads of the next
-// PF stages are in flight in registers while a stage is multiplied.  Two
-// kernels: gemm_body (16 tokens, weights through LDS, 16x16x32 MFMA),
-// gemm_body_ra (64 tokens, weights dequantised into the A operand
-// registers, 32x32x16 MFMA) and gemm_body_wide (128 tokens, weights
-// through LDS, 32x32x16 MFMA).
+// accumulation.  LDS is double-buffered; the global loads of the next PF
+// stages are in flight in registers while a stage is multiplied.  Three
+// kernels: gemm_body_sk16 (16 tokens, four k-splits, weights dequantised
+// into the A operand registers, 16x16x32 MFMA), gemm_body_ra (64 tokens,
+// weights into the A operand registers, 32x32x16 MFMA) and
+// gemm_body_wide (128 tokens, weights through LDS, 32x32x16 MFMA).
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
 enum { XT_F32 = 0, XT_F16 = 1, XT_BF16 = 2 };
 
 // 32 contiguous elements [32j, 32j+32) of a row -> f16 bits, 2 per dword,
@@ -265,9 +265,12 @@ struct XTile {
     }
 };
 
-// Tile shapes.  BN = 16 (up to 16 tokens): gemm_body, a stage of 64 rows x
-// 128 k (8192 weights: one 32-element sub-block per thread of the 256), so a
-// 14336-row weight spreads over 224 workgroups.  BN = 64: gemm_body_ra,
+// Tile shapes.  BN = 16 (up to 16 tokens): gemm_body_sk16, 64 rows per
+// 1024-thread workgroup, so a 14336-row weight spreads over 224
+// workgroups of 16 waves (measured on MI355X, 14336x4096 Q4_K, bf16 X:
+// 18.6 us at m = 16 against 23.0 us for 64-row tiles of 4 waves staging
+// the weights through LDS; deeper rings, x held whole in LDS, or 8 and 4
+// waves per workgroup were slower).  BN = 64: gemm_body_ra,
 // 128 rows (32 per wave) x 64 k per stage, weights dequantised straight
 // into the MFMA operand registers.  BN = 128: gemm_body_wide, 128 x 64
 // stages through LDS on a 2 x 2 wave grid.  PF stages of weights and
@@ -282,123 +285,11 @@ template <> struct GemmTile<16> { static constexpr int BM = 64, PF = 8; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
 
-template <typename D, int BN, int XT, int YT>
-__device__ void gemm_body(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
-                          int m, int n, int k, int ldy) {
-    constexpr int BM = GemmTile<BN>::BM, PF = GemmTile<BN>::PF;
-    constexpr int BK = 8192 / BM;       // k per stage
-    constexpr int KP = BK + 8;          // LDS row pitch in halves (pads away bank conflicts)
-    constexpr int SPR = BK / 32;        // sub-blocks per tile row and stage
-    constexpr int RA = BM / 64;         // 16-row MFMA tiles per wave
-    __shared__ __align__(16) uint16_t wl[2][BM * KP];
-    __shared__ __align__(16) uint16_t xl[2][BN * KP];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int r0 = blockIdx.x * BM, t0 = blockIdx.y * BN;
-    const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
-    const int nk = k / BK;
-
-    // weights: thread t dequantises sub-block SPR*s + (t % SPR) of tile row t / SPR
-    const int wrow = tid / SPR, wsub = tid % SPR;
-    const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
-    // activations: the BN x BK tile of the stage
-    using XS = XTile<XT, BN, BK>;
-    const typename XS::Map xm = XS::map(t0, m, k, KP);
-    struct Stage {
-        typename D::Raw wr;
-        XS xr;
-    };
-    auto issue = [&](Stage& st, int s) {
-        const int sc = min(s, nk - 1);  // stages past the end re-load the last one
-        // never predicated, so the loads retire in order without a drain
-        st.wr = D::load(wp, SPR * sc + wsub);
-        st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
-    };
-
-    float4_t acc[RA][BN / 16];
-#pragma unroll
-    for (int a = 0; a < RA; a++)
-#pragma unroll
-        for (int b = 0; b < BN / 16; b++) acc[a][b] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    Stage ring[PF];
-#pragma unroll
-    for (int i = 0; i < PF; i++) issue(ring[i], i);
-
-    // one stage: dequantised weights and activations -> LDS, then (with
-    // `next`) the loads of stage s + PF into the freed slot, then the MFMAs
-    auto step = [&](Stage& st, int s, bool next) {
-        const int buf = s & 1;
-        {   // dequantised weights -> LDS
-            uint32_t o[16];
-            D::deq(st.wr, SPR * s + wsub, o);
-            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
-#pragma unroll
-            for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-        }
-        st.xr.store(xl[buf], xm);  // activations -> LDS
-        __syncthreads();
-        if (next) issue(st, s + PF);
-        // keep the loads ahead of the MFMAs (the scheduler would otherwise
-        // sink them below, leaving no load in flight during the multiply)
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            const int kof = 32 * ks + 8 * (lane >> 4);
-            half8_t av[RA];
-#pragma unroll
-            for (int a = 0; a < RA; a++)
-                av[a] = *reinterpret_cast<const half8_t*>(
-                    &wl[buf][((BM / 4) * wave + 16 * a + (lane & 15)) * KP + kof]);
-#pragma unroll
-            for (int b = 0; b < BN / 16; b++) {
-                const half8_t bv = *reinterpret_cast<const half8_t*>(&xl[buf][(16 * b + (lane & 15)) * KP + kof]);
-#pragma unroll
-                for (int a = 0; a < RA; a++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[a], bv, acc[a][b], 0, 0, 0);
-            }
-        }
-    };
-    // whole groups of PF stages with no condition in the body (a condition
-    // would make the compiler drain every load at the loop head); stages
-    // past the end are loaded (clamped) and never consumed
-    int base = 0;
-    for (; base + PF <= nk; base += PF) {
-#pragma unroll
-        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
-    }
-#pragma unroll
-    for (int b0 = 0; b0 < PF - 1; b0++)
-        if (base + b0 < nk) step(ring[b0], base + b0, false);
-
-    // lane holds D[4*(lane/16) + i][lane%16] of each 16x16 tile:
-    // weight row r0 + (BM/4)*wave + 16*a + 4*(lane/16) + i, token t0 + 16*b + lane%16
-#pragma unroll
-    for (int a = 0; a < RA; a++) {
-#pragma unroll
-        for (int b = 0; b < BN / 16; b++) {
-            const int tok = t0 + 16 * b + (lane & 15);
-            const int rb = r0 + (BM / 4) * wave + 16 * a + 4 * (lane >> 4);
-            if (tok < m) {
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    if (rb + i < n) {
-                        const size_t off = (size_t)tok * ldy + rb + i;
-                        if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = acc[a][b][i];
-                        else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(acc[a][b][i]);
-                    }
-                }
-            }
-        }
-    }
-}
-
-typedef float float16_t __attribute__((ext_vector_type(16)));
-
 // Wide token tiles (BN = 128): v_mfma_f32_32x32x16_f16 on a 2 x 2 grid
 // of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
 // 128-row tile and tokens [wc BN/2, (wc+1) BN/2) -- so every A fragment
-// read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k
-// as in gemm_body; GemmTile<BN>::PF stages are in flight per workgroup
+// read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k;
+// GemmTile<BN>::PF stages are in flight per workgroup
 // (measured on MI355X, 14336x4096 Q4_K: 64 tokens 52.5 -> 49.0 us from 2
 // to 4 stages, 256 tokens 83 -> 69 us from 1 to 2), and two workgroups
 // share a CU.
@@ -476,7 +367,9 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
                     acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
     };
-    // whole groups of PF stages, then the tail (as in gemm_body)
+    // whole groups of PF stages with no condition in the body (a condition
+    // would make the compiler drain every load at the loop head), then the
+    // tail; stages past the end are loaded (clamped) and never consumed
     int base = 0;
     for (; base + PF <= nk; base += PF) {
 #pragma unroll
@@ -506,6 +399,118 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
         }
     }
 }
+
+// Split-k tiles for up to 16 tokens: a 1024-thread workgroup owns 64
+// weight rows x 16 tokens; wave w takes the 16-row tile w % 4 and the
+// k-split w / 4, whose 128-k stages are s = w / 4, w / 4 + 4, ...  Lane l
+// takes row l % 16 of its tile and dequantises sub-block g = l / 16 of the
+// stage straight into its A operand registers; v_mfma_f32_16x16x32_f16
+// step q uses elements [8q, 8q+8) of it, so its B fragment is x[32g + 8q,
+// +8) of token l % 16, read from the split's activation tile in LDS (the
+// split's four waves stage it together).  Sixteen waves per CU keep the
+// weight stream of a 224-workgroup grid in flight; the four splits' partial
+// tiles are summed through LDS at the end.
+template <typename D, int XT, int YT, int PF, int RT>
+__device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
+                               int m, int n, int k, int ldy) {
+    constexpr int ES = XT == XT_F32 ? 4 : 2, KP = 136;  // tile pitch in halves (pads away bank conflicts)
+    constexpr int NW = 4 * RT;                           // waves: RT row tiles x 4 k-splits
+    constexpr int E = 32 / RT;                           // x elements per lane and stage
+    constexpr int XW = E * ES / 16;                      // 16-byte x loads per lane and stage
+    __shared__ __align__(16) uint16_t xl[2][4][16 * KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rt = wave % RT, ks = wave / RT, g = lane >> 4;
+    const int r0 = blockIdx.x * (16 * RT), t0 = blockIdx.y * 16;
+    const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const int nk = k / 128, cnt = (nk + 3) >> 2;  // every wave runs cnt steps (a uniform barrier count)
+    const uint8_t* wp = w + (size_t)min(r0 + 16 * rt + (lane & 15), n - 1) * row_bytes;
+    // this lane's share of the split's x tile: E elements of one token
+    const int lt = 64 * rt + lane, xtok = (lt * E) >> 7, xk = (lt * E) & 127;
+    const uint8_t* xp = static_cast<const uint8_t*>(x) + ((size_t)min(t0 + xtok, m - 1) * k + xk) * ES;
+    struct Stage {
+        typename D::Raw wr;
+        uint4 xr[XW];
+    };
+    auto issue = [&](Stage& st, int i) {
+        const int s = min(ks + 4 * i, nk - 1);  // past the split's last stage: re-load the last one
+        st.wr = D::load(wp, 4 * s + g);
+#pragma unroll
+        for (int j = 0; j < XW; j++) st.xr[j] = reinterpret_cast<const uint4*>(xp + (size_t)s * 128 * ES)[j];
+    };
+    float4_t acc = float4_t{0.f, 0.f, 0.f, 0.f};
+    Stage ring[PF];
+#pragma unroll
+    for (int i = 0; i < PF; i++) issue(ring[i], i);
+    auto step = [&](Stage& st, int i, bool next) {
+        const int buf = i & 1;
+        // the lane's activations -> f16 in the split's tile
+        uint4* dst = reinterpret_cast<uint4*>(&xl[buf][ks][xtok * KP + xk]);
+        if constexpr (XT == XT_F32) {
+#pragma unroll
+            for (int j = 0; j < XW / 2; j++) {
+                const uint4 a = st.xr[2 * j], b = st.xr[2 * j + 1];
+                dst[j] = make_uint4(f2h2(__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, a.y)),
+                                    f2h2(__builtin_bit_cast(float, a.z), __builtin_bit_cast(float, a.w)),
+                                    f2h2(__builtin_bit_cast(float, b.x), __builtin_bit_cast(float, b.y)),
+                                    f2h2(__builtin_bit_cast(float, b.z), __builtin_bit_cast(float, b.w)));
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < XW; j++) {
+                const uint32_t v[4] = {st.xr[j].x, st.xr[j].y, st.xr[j].z, st.xr[j].w};
+                uint32_t o[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    o[e] = XT == XT_F16 ? v[e]
+                                        : f2h2(__builtin_bit_cast(float, v[e] << 16),
+                                               __builtin_bit_cast(float, v[e] & 0xffff0000u));
+                dst[j] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+        uint32_t o[16];
+        D::deq(st.wr, 4 * min(ks + 4 * i, nk - 1) + g, o);
+        __syncthreads();
+        if (next) issue(st, i + PF);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 4 * i < nk) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const half8_t bv =
+                    *reinterpret_cast<const half8_t*>(&xl[buf][ks][(lane & 15) * KP + 32 * g + 8 * q]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    __builtin_bit_cast(half8_t, make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3])), bv,
+                    acc, 0, 0, 0);
+            }
+        }
+    };
+    int base = 0;
+    for (; base + PF <= cnt; base += PF) {
+#pragma unroll
+        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
+    }
+#pragma unroll
+    for (int b0 = 0; b0 < PF - 1; b0++)
+        if (base + b0 < cnt) step(ring[b0], base + b0, false);
+
+    // lane l holds D[row 4(l/16) + i][token l%16] of its tile; sum the splits
+    __syncthreads();
+    float* red = reinterpret_cast<float*>(&xl[0][0][0]);  // [NW waves][256]
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave * 256 + (4 * g + i) * 16 + (lane & 15)] = acc[i];
+    __syncthreads();
+    for (int o = tid; o < 256 * RT; o += 64 * NW) {
+        const int orow = o >> 4, otok = o & 15, ot = orow >> 4, oi = (orow & 15) * 16 + otok;
+        const float v = (red[ot * 256 + oi] + red[(RT + ot) * 256 + oi]) +
+                        (red[(2 * RT + ot) * 256 + oi] + red[(3 * RT + ot) * 256 + oi]);
+        const int row = r0 + orow, tok = t0 + otok;
+        if (row < n && tok < m) {
+            const size_t off = (size_t)tok * ldy + row;
+            if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = v;
+            else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(v);
+        }
+    }
+}
+
 
 // Register-A tiles: each wave owns RW weight rows (RW / 32 tiles of 32
 // rows) and all BN tokens of the workgroup's tile, and dequantises its own
@@ -611,6 +616,14 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
     }
 }
 
+// Stages in flight for gemm_body_sk16 (128 registers per thread): two
+// where a stage (raw sub-block + the lane's activation words) takes at most
+// 16 registers, else one
+template <typename D, int XT>
+constexpr int sk16_pf() {
+    return (int)(sizeof(typename D::Raw) / 4) + (XT == XT_F32 ? 8 : 4) <= 16 ? 2 : 1;
+}
+
 // Stages in flight for gemm_body_ra: GemmTile<BN>::PF, fewer where a stage
 // (the raw weight sub-block plus the thread's activation words) is so large
 // that the ring would spill to scratch memory.
@@ -627,10 +640,10 @@ constexpr int ra_pf() {
 
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(256, BN == 16 ? 1 : 2) void                             \
+    extern "C" __global__ __launch_bounds__(BN == 16 ? 1024 : 256, BN == 16 ? 1 : 2) void           \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
-        if constexpr (BN == 16) gemm_body<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                   \
+        if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, sk16_pf<D, XT>(), 4>(x, w, y, m, n, k, ldy); \
         else if constexpr (BN == 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
         else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
     }
