@@ -186,6 +186,7 @@ struct GemvPlan {
     unsigned grid;   // workgroups of kGemvThreads threads
     unsigned lds;    // dynamic LDS bytes: x as two int8 planes + padding, scales, sums
     bool ring;       // item-ring main loop (_ring kernels)
+    bool ringl;      // stepped item ring for long rows (_ringl kernels, launched with one unit per step)
 };
 
 // matches xstage_bytes() in gguf_gemv.hip
@@ -223,8 +224,15 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     // faster from about 8 MB of weights up; smaller ones are latency-bound
     // and finish sooner with the plain double buffer)
     const double wbytes = (double)n * (double)(k / F->block_elems) * F->block_bytes;
-    const bool ring = !pair && rows == 1 && it <= 2 && (ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6));
-    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring};
+    const bool big = ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6);
+    const bool ring = !pair && rows == 1 && it <= 2 && big;
+    // the longest rows of large matrices (8 units per lane): the stepped
+    // ring, one unit per lane and step.  Measured on MI355X at 4096x14336:
+    // Q8_0 18.3 -> 16.8 us, Q6_K 17.7 -> 15.5, Q4_0 13.7 -> 12.4; at 4
+    // units per lane the double buffer stays faster (Q4_K 9.6 against
+    // 11.6, Q5_K 12.9 against 13.9, Q8_0 14336x8192 28.5 against 29.4).
+    const bool ringl = !pair && rows == 1 && it == 8 && big;
+    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
 }
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
@@ -259,6 +267,8 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
                     p.iters);
     bool epi = ba != nullptr || bb != nullptr || mode == 1;
     const char* kind_sfx = pair ? "_pair" : "";
+    if (kind != GK_PLAIN) p.ringl = false;  // built for plain and _epi only
+    if (p.ringl) p.iters = 1;
     if (kind == GK_ATT) p.ring = false;
     if (kind == GK_ATT) {
         kind_sfx = "_att";
@@ -272,7 +282,8 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
         if (epi) return fail(CIMA_E_INVALID, "%s: the argmax GEMV takes no bias or residual", api);
     }
     snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s%s", F->name, p.rows, p.iters,
-             act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : "", kind_sfx, epi ? "_epi" : "");
+             act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : (p.ringl ? "_ringl" : ""), kind_sfx,
+             epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
     int resident = 0;
@@ -281,7 +292,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (resident < 1) resident = 1;
     // persistent grid: one workgroup per CU for the item ring and for Q8_0,
     // two otherwise (measured on MI355X)
-    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : ((p.ring || t == CIMA_GGML_Q8_0) ? 1 : 2);
+    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2);
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;
@@ -359,6 +370,11 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                 snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
                 if (!rc) rc = add(F->gemv_module, name);
             }
+        for (const char* rk : {"_f32_ringl", "_f32_ringl_epi", "_f16_ringl", "_f16_ringl_epi"}) {
+            char name[96];
+            snprintf(name, sizeof name, "cima_gemv_%s_r1_i1%s", F->name, rk);
+            if (!rc) rc = add(F->gemv_module, name);
+        }
         for (int bn : kGemmBN)
             for (const char* xt : {"f32", "f16", "bf16"})
                 for (const char* yt : {"f32", "f16"}) {

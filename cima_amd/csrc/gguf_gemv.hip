@@ -1,17 +1,18 @@
-// Fused GGUF dequant-GEMV for gfx950 (CDNA4): the code object cima_gemv.hsaco,
-// loaded by the host library with hipModuleLoad and launched with
-// hipModuleLaunchKernel.  Counterpart of the reference's
-// k_gguf_<fmt>_gemv + GEMV_TAIL (src/kernels.cu:1057-1313) and of the f16
-// GEMV's epilogue modes (src/kernels.cu:493-538), for Q8_0, Q4_0, Q4_K and
-// Q6_K weights kept in their GGUF block layout.
+// Fused GGUF dequant-GEMV for gfx950 (CDNA4), compiled once per format set
+// into the code objects cima_gemv_a/b/c.hsaco, loaded by the host library
+// with hipModuleLoad and launched with hipModuleLaunchKernel.  Counterpart
+// of the reference's k_gguf_<fmt>_gemv + GEMV_TAIL (src/kernels.cu:
+// 1057-1313) and of the f16 GEMV's epilogue modes (src/kernels.cu:493-538),
+// for the nine GGUF block formats, weights kept in their block layout.
 //
-// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_ring][_pair|_att|_amax][_epi]
+// Kernel names: cima_gemv_<fmt>_r<R>_i<ITERS>_<f32|f16>[_ring|_ringl][_pair|_att|_amax][_epi]
 //   R      rows per lane group, ITERS unit steps per row and lane
 //   f32/16 activation, bias and output type
 //   _pair  SwiGLU over a gate and an up weight
 //   _att   x merged from split-attention partials (o projection)
 //   _amax  outputs also reduced into a greedy argmax (head)
 //   _ring  item-ring main loop (deeper prefetch; tall one-unit-row matrices)
+//   _ringl stepped item ring (long rows: several steps of ITERS units per row)
 //   _epi   bias and/or residual (mode 1) operands present
 // Every variant can take an RMSNorm prologue (GemvExt::norm_w).
 #include <type_traits>
@@ -718,8 +719,8 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     const void* p2 = has2 ? (PAIR ? bias_b : static_cast<const void*>(y)) : x;
 
     // x chunks per thread for the longest row this variant serves (ITERS
-    // units of 64 lanes): k / 16 / GNT
-    constexpr int XB = (ITERS * F::UE * 4 + GNT - 1) / GNT;
+    // units of 64 lanes; 8 for the stepped item ring): k / 16 / GNT
+    constexpr int XB = ((RING == 2 ? 8 : ITERS) * F::UE * 4 + GNT - 1) / GNT;
     // x -> LDS; the caller has the first weights in flight (and, for plain
     // x, x's first batch ahead of them in `xb`)
     auto stage = [&](XBatch<ACT, XB>& xb) {
@@ -798,7 +799,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #endif
     };
 
-    if constexpr (RING) {
+    if constexpr (RING == 1) {
         // Item ring (single-row rows of one or two units per lane): item q
         // is the lane's q-th row group; DEPTH items are in flight in a ring
         // of slots and the loop body is unrolled over DEPTH items so slot
@@ -844,6 +845,81 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                 issue(ring[b], base + b + DEPTH);
             }
         }
+    } else if constexpr (RING == 2) {
+        // Stepped item ring (long rows): a row group takes T steps of ITERS
+        // units per lane, and an item is one step of one row group -- the
+        // lane's q-th item is step q % T of its (q / T)-th row group.  Items
+        // flow through the same ring of DEPTH slots across row-group
+        // boundaries; x is read from LDS per item (the units differ per
+        // step), the partial sums carry over the steps, and the last step
+        // of a row group reduces and writes it.  Items past the lane's last
+        // row group re-load it and write nothing.
+        static_assert(ITERS <= 2 && R == 1, "the stepped item ring serves one-row groups");
+        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
+        const int T = (U + (ITERS << lpr_shift) - 1) / (ITERS << lpr_shift);
+        const int items = per * T;
+        struct Item {
+            typename F::Raw w[S][ITERS];
+            float e1[R], e2[R];
+        };
+        int ii = 0, is = 0;  // next item to load: row group, step
+        auto issue = [&](Item& dst) {
+            const int g = min(gid + ii * ngroups, rg_last);
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                const int row = min(g * R + (s % R), n - 1);
+                const uint8_t* rp = ((PAIR && s >= R) ? wb : wa) + (size_t)row * row_bytes;
+#pragma unroll
+                for (int j = 0; j < ITERS; j++)
+                    dst.w[s][j] = F::load(rp, min(li + ((is * ITERS + j) << lpr_shift), U - 1));
+            }
+            if constexpr (EPI) epi_load(dst.e1, dst.e2, g);
+            if (++is == T) {
+                is = 0;
+                ++ii;
+            }
+        };
+        int ci = 0, cs = 0;  // next item to compute
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) acc[s] = 0.f;
+        auto consume = [&](const Item& src) {
+#pragma unroll
+            for (int j = 0; j < ITERS; j++) {
+                const int u = li + ((cs * ITERS + j) << lpr_shift);
+                typename F::Xf xf;
+                F::loadx(xq, xs, xsum, min(u, U - 1), xf);
+#pragma unroll
+                for (int s = 0; s < S; s++) {
+                    const float p = wdot(src.w[s][j], xf, min(u, U - 1));
+                    acc[s] += u < U ? p : 0.f;
+                }
+            }
+            if (++cs == T) {
+                finish(acc, src.e1, src.e2, ci);
+#pragma unroll
+                for (int s = 0; s < S; s++) acc[s] = 0.f;
+                cs = 0;
+                ++ci;
+            }
+        };
+        Item ring[DEPTH];
+        XBatch<ACT, XB> xb;
+        if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) issue(ring[d]);
+        stage(xb);
+        int base = 0;
+        for (; base + DEPTH <= items; base += DEPTH) {
+#pragma unroll
+            for (int b = 0; b < DEPTH; b++) {
+                consume(ring[b]);
+                issue(ring[b]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < DEPTH - 1; b++)
+            if (base + b < items) consume(ring[b]);
     } else {
         // Row-group double buffer: a lane holds all ITERS units of a row
         // group; the next row group is loaded while the current one is
@@ -950,7 +1026,14 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring, F, 1, IT, ACT_F16, 0, 0, 0, 0, 1)                  \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 1)              \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_amax, F, 1, IT, ACT_F16, 0, 0, 0, 1, 1)
-#define GEMV_RING(FN, F) GEMV_RING_IT(FN, F, 1) GEMV_RING_IT(FN, F, 2)
+// stepped item-ring variants (long rows, k up to the i8 kernels'):
+// cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ringl[_epi]
+#define GEMV_RINGL_IT(FN, F, IT)                                                                       \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ringl, F, 1, IT, ACT_F32, 0, 0, 0, 0, 2)                 \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ringl_epi, F, 1, IT, ACT_F32, 0, 1, 0, 0, 2)             \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ringl, F, 1, IT, ACT_F16, 0, 0, 0, 0, 2)                 \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ringl_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 2)
+#define GEMV_RING(FN, F) GEMV_RING_IT(FN, F, 1) GEMV_RING_IT(FN, F, 2) GEMV_RINGL_IT(FN, F, 1)
 
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \

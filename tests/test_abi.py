@@ -54,6 +54,8 @@ def test_code_object_holds_every_kernel():
         for it in (1, 2):
             for rk in ("_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"):
                 assert f"cima_gemv_{f}_r1_i{it}{rk}".encode() in blob
+        for rk in ("_f32_ringl", "_f32_ringl_epi", "_f16_ringl", "_f16_ringl_epi"):
+            assert f"cima_gemv_{f}_r1_i1{rk}".encode() in blob
         assert f"cima_dequant_{f}".encode() in blobs["dequant"]
         assert f"cima_gather_{f}".encode() in blobs["dequant"]
         for bn in (16, 64, 128):
@@ -211,6 +213,7 @@ def test_hot_gemv_kernels_do_not_spill():
            for a in ("f32", "f16") for sfx in ("", "_epi", "_pair")]
     hot += [f"cima_gemv_{f}_r1_i{it}_{a}_ring{e}" for f in fmts for it in (1, 2)
             for a in ("f32", "f16") for e in ("", "_epi")]
+    hot += [f"cima_gemv_{f}_r1_i1_{a}_ringl{e}" for f in fmts for a in ("f32", "f16") for e in ("", "_epi")]
     hot += [f"cima_gemv_{f}_r1_i1_f16_{v}" for f in ("q8_0", "q4_k") for v in ("att_epi", "amax", "ring_amax")]
     spills = {k: notes[k] for k in hot if notes[k][1] > 0}
     assert not spills, spills

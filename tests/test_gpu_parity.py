@@ -389,10 +389,11 @@ def test_launches_order_with_torch_default_stream(hip):
 
 @pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
 def test_item_ring_matches_double_buffer(t):
-    """The item-ring main loop (forced on with CIMA_GEMV_RING=1, forced off
-    with 2) computes every row exactly as the row-group double buffer does:
+    """The item-ring main loops (forced on with CIMA_GEMV_RING=1, forced off
+    with 2) compute every row exactly as the row-group double buffer does:
     identical outputs, f32 and f16, with and without the epilogue, for rows
-    of one and of two units per lane (ragged included)."""
+    of one and of two units per lane and for long rows of several steps
+    (ragged included)."""
     import os
     from cima_amd.hip import HipCtx
 
@@ -406,8 +407,10 @@ def test_item_ring_matches_double_buffer(t):
         ctxs[mode].use_torch_stream()
     be = mg.BLOCK[t][0]
     ue = 64 if be == 256 else 32  # elements per unit
-    # one unit per lane at 32 lanes; two per lane at 64 (ragged: 100 units)
-    for n, k in ((1, 32 * ue), (37, 32 * ue), (1000, 32 * ue), (37, 128 * ue), (300, 100 * ue)):
+    # one unit per lane at 32 lanes; two per lane at 64 (ragged: 100 units);
+    # long rows of 4-7 steps of 64 units (the stepped ring; ragged: 200, 300)
+    for n, k in ((1, 32 * ue), (37, 32 * ue), (1000, 32 * ue), (37, 128 * ue), (300, 100 * ue), (37, 200 * ue),
+                 (300, 448 * ue), (1, 300 * ue)):
         w = torch.from_numpy(synth.weights(t, 80 + n, 0.02, n, k)).cuda()
         for dt in (torch.float32, torch.float16):
             x = torch.from_numpy(synth.normal(81, 1.0, k)).to(dt).cuda()
