@@ -110,6 +110,7 @@ struct cima_hip_ctx {
     int tune_wgs = 0;  // workgroups per CU of the persistent grid (0 = built-in default)
     int tune_gemm_bn = 0;  // prefill GEMM token tile (0 = smallest built one covering m)
     int tune_ring = 0;     // GEMV main loop: 0 = heuristic, 1 = item ring where built, 2 = never
+    int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
 };
@@ -225,13 +226,14 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     // and finish sooner with the plain double buffer)
     const double wbytes = (double)n * (double)(k / F->block_elems) * F->block_bytes;
     const bool big = ctx->tune_ring == 1 || (ctx->tune_ring == 0 && wbytes >= 8e6);
-    const bool ring = !pair && rows == 1 && it <= 2 && big;
     // the longest rows of large matrices (8 units per lane): the stepped
     // ring, one unit per lane and step.  Measured on MI355X at 4096x14336:
     // Q8_0 18.3 -> 16.8 us, Q6_K 17.7 -> 15.5, Q4_0 13.7 -> 12.4; at 4
     // units per lane the double buffer stays faster (Q4_K 9.6 against
     // 11.6, Q5_K 12.9 against 13.9, Q8_0 14336x8192 28.5 against 29.4).
-    const bool ringl = !pair && rows == 1 && it == 8 && big;
+    const bool ringl = !pair && rows == 1 && big && ctx->tune_ringl != 2 &&
+                       (it == 8 || (ctx->tune_ringl == 1 && it >= 2));
+    const bool ring = !pair && rows == 1 && it <= 2 && big && !ringl;
     return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
 }
 
@@ -414,6 +416,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_LPR")) el = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
