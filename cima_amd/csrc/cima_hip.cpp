@@ -1016,13 +1016,25 @@ int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, cons
             return fail(CIMA_E_INVALID, "%s: k=%d does not leave room for the pair table in LDS", api, k);
         if (ctx->tune_nf4_kernel == 2) tab = false;
         const int wpg = tab ? 16 : 4;  // waves per workgroup
-        // measured on MI355X (4096-128256 rows, k 4096 and 14336): the table
-        // kernel with one row per wave and two workgroups per CU where the
-        // LDS holds them was the fastest or within 5% of it
+        // two workgroups per CU where the LDS holds them; rows per wave: the
+        // fewest row-steps for the busiest wave, ties to 2 rows, then 1
+        // (measured on MI355X, weights cold: 14336x4096 9.9 us at 2 rows
+        // against 10.7 at 1; 4096x14336, one workgroup per CU, 10.7 at 1
+        // row against 13.8 at 2)
         const long long wgs = ctx->tune_wgs ? ctx->tune_wgs : (!tab || 2 * tab_lds <= ctx->max_lds ? 2 : 1);
         const long long waves = wgs * ctx->num_cu * wpg;
         int r = ctx->tune_nf4_rows;
-        if (!r) r = tab ? 1 : ((n + 3) / 4 >= waves ? 4 : ((n + 1) / 2 >= waves ? 2 : 1));
+        if (!r) {
+            long long best = -1;
+            for (int cand : {2, 1, 4}) {
+                const long long groups_c = (n + cand - 1) / cand;
+                const long long cost = (groups_c + waves - 1) / waves * cand;
+                if (best < 0 || cost < best) {
+                    best = cost;
+                    r = cand;
+                }
+            }
+        }
         const long long groups = (n + r - 1) / r;
         long long grid = (groups + wpg - 1) / wpg;
         if (grid > wgs * ctx->num_cu) grid = wgs * ctx->num_cu;
