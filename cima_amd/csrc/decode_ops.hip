@@ -207,10 +207,14 @@ DEV void attn_chunk(AttnLds<D>& L, const AttnRegs<D>& R, int s0, int s1, int sne
 #pragma unroll
             for (int i = 0; i < 8; i++) a[i] += pr * L.vn[8 * pc + i];
         } else {
+            // rows past the chunk's live length hold clamped copies of
+            // another row (possibly the new position's stale cache row,
+            // which may hold anything): selected away, not multiplied by 0
+            const bool live_row = row < len;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                a[2 * i] += pr * h2f(w[i] & 0xffffu);
-                a[2 * i + 1] += pr * h2f(w[i] >> 16);
+                a[2 * i] += live_row ? pr * h2f(w[i] & 0xffffu) : 0.f;
+                a[2 * i + 1] += live_row ? pr * h2f(w[i] >> 16) : 0.f;
             }
         }
     }

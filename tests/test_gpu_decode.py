@@ -175,21 +175,24 @@ def test_attn_split_and_reduce(hip, dim, qh, kvh, seq, csz, window):
             assert np.allclose(P[h, c, 2:], acc, rtol=1e-3, atol=1e-3 * l)
 
 
+@pytest.mark.parametrize("fill", ["zero", "nan"])
 @pytest.mark.parametrize("dim,qh,kvh,pos,csz", [(64, 14, 2, 2048, 256), (64, 14, 2, 0, 256), (128, 32, 8, 300, 128),
                                                 (64, 14, 2, 255, 256), (64, 14, 2, 256, 256), (64, 14, 2, 1000, 64)])
-def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz):
+def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz, fill):
     """rope q, k + append + split in one launch, merged by attn_reduce, ==
-    the separate ops; and the merge folded into the o-projection GEMV."""
+    the separate ops; and the merge folded into the o-projection GEMV.  The
+    cache rows past the position and the partials buffer start as zeros or
+    as NaN: the kernels load them speculatively and must not let them in."""
     max_seq = 4096
     nch = max_seq // csz
     r = np.random.default_rng(pos + dim)
-    kc = np.zeros((kvh, max_seq, dim), np.float16)
-    vc = np.zeros_like(kc)
+    kc = np.full((kvh, max_seq, dim), 0.0 if fill == "zero" else np.nan, np.float16)
+    vc = kc.copy()
     kc[:, :pos] = r.normal(size=(kvh, pos, dim))
     vc[:, :pos] = r.normal(size=(kvh, pos, dim))
     qkv = (0.5 * r.normal(size=(qh + 2 * kvh) * dim)).astype(np.float16)
     dkc, dvc = dev16(kc), dev16(vc)
-    part = torch.zeros(qh * nch * (dim + 2), device="cuda")
+    part = torch.full((qh * nch * (dim + 2),), 0.0 if fill == "zero" else float("nan"), device="cuda")
     out = torch.empty((qh, dim), dtype=torch.float16, device="cuda")
     posd = torch.tensor([pos], dtype=torch.int32, device="cuda")
     scale = 1 / np.sqrt(dim)
@@ -206,7 +209,8 @@ def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz):
     gk = host(dkc)
     assert ulps_ok(gk[:, pos], wk[:, pos], ulps=2, atol=2e-4)
     assert np.all(host(dvc)[:, pos] == wv[:, pos])
-    assert np.all(gk[:, :pos] == kc[:, :pos]) and np.all(gk[:, pos + 1:] == 0)
+    assert np.all(gk[:, :pos] == kc[:, :pos])
+    assert np.array_equal(gk[:, pos + 1:], kc[:, pos + 1:], equal_nan=True)
     # the same partials merged inside the o projection (mode 1 residual)
     n = 300
     w = synth.weights(Q8_0, 40 + dim, 0.02, n, qh * dim)
