@@ -1,14 +1,17 @@
 // Host side of the C ABI declared in include/cima_hip.h.
 //
-// The library loads three gfx950 code objects (cima_gemv / cima_gemm /
-// cima_dequant .hsaco, built from gguf_*.hip with hipcc --genco) through
-// hipModuleLoad and launches their kernels with hipModuleLaunchKernel -- the
-// HIP counterpart of the reference's CudaCtx (src/cuda.rs), which
-// JIT-compiles kernels.cu with NVRTC and launches through cuLaunchKernel
-// (src/cuda.rs:1112-1151).  No call allocates device memory.
+// The library loads seven gfx950 code objects (kModuleFiles, built from the
+// .hip sources with hipcc --genco) through hipModuleLoad and launches their
+// kernels with hipModuleLaunchKernel -- the HIP counterpart of the
+// reference's CudaCtx (src/cuda.rs), which JIT-compiles kernels.cu with
+// NVRTC and launches through cuLaunchKernel (src/cuda.rs:1112-1151).  No
+// call allocates device memory; the library route of
+// cima_hip_gguf_gemm_slab creates a hipBLASLt handle and plan on its first
+// call of a shape.
 #include "cima_hip.h"
 
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <dlfcn.h>
 #include <stdarg.h>
@@ -18,7 +21,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <map>
+#include <mutex>
 #include <string>
+#include <tuple>
 #include <unordered_map>
 
 namespace {
@@ -113,6 +119,11 @@ struct cima_hip_ctx {
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
+    int gemm_lib_min = 0;     // dequant-slab prefill: fewest tokens routed to the library GEMM (0 = 257)
+    int last_gemm_route = 0;  // route of the last gguf_gemm_slab call: 0 fused MFMA kernel, 1 slab + library
+    void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
+    // cached library plans: (m, n, k, y dtype, workspace cap) -> plan
+    std::map<std::tuple<int, int, int, int, size_t>, struct LtPlan*> lt_plans;
 };
 
 namespace {
@@ -152,6 +163,83 @@ std::string default_code_dir() {
         return s == std::string::npos ? std::string(".") : p.substr(0, s);
     }
     return ".";
+}
+
+// hipBLASLt, opened with dlopen on first use (as the reference dlopens
+// cuBLAS, src/cuda.rs:311-404): a host without it keeps every entry point
+// except the library route of cima_hip_gguf_gemm_slab, which then runs the
+// fused kernel.
+struct LtApi {
+    bool ok = false;
+    decltype(&hipblasLtCreate) create = nullptr;
+    decltype(&hipblasLtDestroy) destroy = nullptr;
+    decltype(&hipblasLtMatmulDescCreate) desc_create = nullptr;
+    decltype(&hipblasLtMatmulDescDestroy) desc_destroy = nullptr;
+    decltype(&hipblasLtMatmulDescSetAttribute) desc_set = nullptr;
+    decltype(&hipblasLtMatrixLayoutCreate) layout_create = nullptr;
+    decltype(&hipblasLtMatrixLayoutDestroy) layout_destroy = nullptr;
+    decltype(&hipblasLtMatmulPreferenceCreate) pref_create = nullptr;
+    decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
+    decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
+    decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
+    decltype(&hipblasLtMatmul) matmul = nullptr;
+};
+
+const LtApi& lt_api() {
+    static LtApi api;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        void* so = dlopen("libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
+        if (!so) so = dlopen("libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
+        if (!so) return;
+        bool ok = true;
+        auto sym = [&](auto& f, const char* name) {
+            f = reinterpret_cast<std::remove_reference_t<decltype(f)>>(dlsym(so, name));
+            ok = ok && f;
+        };
+        sym(api.create, "hipblasLtCreate");
+        sym(api.destroy, "hipblasLtDestroy");
+        sym(api.desc_create, "hipblasLtMatmulDescCreate");
+        sym(api.desc_destroy, "hipblasLtMatmulDescDestroy");
+        sym(api.desc_set, "hipblasLtMatmulDescSetAttribute");
+        sym(api.layout_create, "hipblasLtMatrixLayoutCreate");
+        sym(api.layout_destroy, "hipblasLtMatrixLayoutDestroy");
+        sym(api.pref_create, "hipblasLtMatmulPreferenceCreate");
+        sym(api.pref_destroy, "hipblasLtMatmulPreferenceDestroy");
+        sym(api.pref_set, "hipblasLtMatmulPreferenceSetAttribute");
+        sym(api.heuristic, "hipblasLtMatmulAlgoGetHeuristic");
+        sym(api.matmul, "hipblasLtMatmul");
+        api.ok = ok;  // the library stays mapped for the life of the process
+    });
+    return api;
+}
+
+}  // namespace
+
+// one library GEMM shape: D[m, n] (row-major, ld n) = X[m, k] W[n, k]^T in
+// hipBLASLt's column-major terms D^T (n x m) = op_T(W^T as k x n) X^T (k x m)
+struct LtPlan {
+    bool ok = false;  // false: the library offers no algorithm (the fused kernel runs)
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws = 0;
+};
+
+namespace {
+
+void lt_release(cima_hip_ctx* ctx) {
+    const LtApi& L = lt_api();
+    for (auto& kv : ctx->lt_plans) {
+        LtPlan* p = kv.second;
+        if (p->desc) (void)L.desc_destroy(p->desc);
+        for (auto l : {p->a, p->b, p->d})
+            if (l) (void)L.layout_destroy(l);
+        delete p;
+    }
+    ctx->lt_plans.clear();
+    if (ctx->lt) (void)L.destroy((hipblasLtHandle_t)ctx->lt);
+    ctx->lt = nullptr;
 }
 
 void unload(cima_hip_ctx* ctx) {
@@ -388,6 +476,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_gather_") + F->name);
     }
     if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
+    if (!rc) rc = add(MOD_DEQUANT, "cima_x_to_f16");
     for (const char* kn : {"cima_nf4_dequant_v", "cima_nf4_dequant_e", "cima_nf4_gemv_e_f16_f16",
                            "cima_nf4_gemv_e_f32_f32"})
         if (!rc) rc = add(MOD_BNB4, kn);
@@ -434,6 +523,7 @@ int cima_hip_destroy(cima_hip_ctx* ctx) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
     }
+    lt_release(ctx);
     unload(ctx);
     delete ctx;
     return 0;
@@ -547,9 +637,13 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int t, const void* x, const voi
     return gemv_common(ctx, t, x, wg, wu, bg, bu, y, n, k, 2, act, true, "cima_hip_gguf_gemv_swiglu");
 }
 
-int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
-                       int ldy, int x_dtype, int y_dtype) {
-    const char* api = "cima_hip_gguf_gemm";
+namespace {
+
+// argument checks shared by the two prefill GEMM entry points; on 0, *Fo is
+// the format, or null for an empty (m or n == 0) call
+int gemm_check(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
+               int x_dtype, int y_dtype, const char* api, const Fmt** Fo) {
+    *Fo = nullptr;
     if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
     const Fmt* F = fmt_of(t);
     if (!F) return fail(CIMA_E_FORMAT, "%s: ggml type %d is not a supported GGUF block format", api, t);
@@ -566,6 +660,13 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
     if (!aligned(x, 16) || !aligned(w, F->w_align) || !aligned(y, 4))
         return fail(CIMA_E_INVALID, "%s: misaligned pointer (x 16 B, %s weights %d B, y 4 B)", api, F->name,
                     F->w_align);
+    *Fo = F;
+    return 0;
+}
+
+// the fused MFMA dequant-GEMM (gguf_gemm.hip) on checked arguments
+int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
+               int x_dtype, int y_dtype, const char* api) {
     // token tile (measured on MI355X, 14336x4096 Q4_K): 16 up to 32 tokens
     // (two 16-token tiles at 33.6 us against 40.2 us for one 64-token tile),
     // 64 up to 128 (twice the workgroups of 128-token tiles), 128 beyond;
@@ -590,6 +691,128 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
                                          1, 0, ctx->stream, args, nullptr);
     return e == hipSuccess ? 0 : hip_fail(e, api);
 }
+
+}  // namespace
+
+int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
+                       int ldy, int x_dtype, int y_dtype) {
+    const char* api = "cima_hip_gguf_gemm";
+    const Fmt* F = nullptr;
+    int rc = gemm_check(ctx, t, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api, &F);
+    if (rc || !F) return rc;
+    return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
+}
+
+namespace {
+
+const size_t kLtWorkspaceMax = 32u << 20;  // library GEMM workspace taken from the slab's tail
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// builds (once per shape) the hipBLASLt descriptors and the algorithm the
+// library's heuristic ranks first for them
+int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, LtPlan** out) {
+    const LtApi& L = lt_api();
+    auto key = std::make_tuple(m, n, k, y_dtype, ws_cap);
+    auto it = ctx->lt_plans.find(key);
+    if (it != ctx->lt_plans.end()) {
+        *out = it->second;
+        return 0;
+    }
+    if (!ctx->lt) {
+        hipblasLtHandle_t h = nullptr;
+        if (L.create(&h) != HIPBLAS_STATUS_SUCCESS)
+            return fail(CIMA_E_LIBRARY, "cima_hip_gguf_gemm_slab: hipblasLtCreate failed");
+        ctx->lt = h;
+    }
+    LtPlan* p = new LtPlan();
+    ctx->lt_plans[key] = p;
+    const hipDataType yt = y_dtype == CIMA_DT_F32 ? HIP_R_32F : HIP_R_16F;
+    const int32_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+    bool ok = L.desc_create(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+              L.desc_set(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
+              L.desc_set(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
+              L.layout_create(&p->a, HIP_R_16F, (uint64_t)k, (uint64_t)n, k) == HIPBLAS_STATUS_SUCCESS &&
+              L.layout_create(&p->b, HIP_R_16F, (uint64_t)k, (uint64_t)m, k) == HIPBLAS_STATUS_SUCCESS &&
+              L.layout_create(&p->d, yt, (uint64_t)n, (uint64_t)m, n) == HIPBLAS_STATUS_SUCCESS;
+    if (ok) {
+        hipblasLtMatmulPreference_t pref = nullptr;
+        uint64_t cap = ws_cap;
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int found = 0;
+        ok = L.pref_create(&pref) == HIPBLAS_STATUS_SUCCESS &&
+             L.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof cap) == HIPBLAS_STATUS_SUCCESS &&
+             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, 1, res, &found) ==
+                 HIPBLAS_STATUS_SUCCESS &&
+             found > 0 && res[0].workspaceSize <= ws_cap;
+        if (pref) (void)L.pref_destroy(pref);
+        if (ok) {
+            p->algo = res[0].algo;
+            p->ws = res[0].workspaceSize;
+        }
+    }
+    p->ok = ok;
+    *out = p;
+    return 0;
+}
+
+}  // namespace
+
+int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
+                            int ldy, int x_dtype, int y_dtype, void* slab, unsigned long long slab_bytes) {
+    const char* api = "cima_hip_gguf_gemm_slab";
+    if (ctx) ctx->last_gemm_route = 0;
+    const Fmt* F = nullptr;
+    int rc = gemm_check(ctx, t, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api, &F);
+    if (rc || !F) return rc;
+    if (slab_bytes && (!slab || !aligned(slab, 256)))
+        return fail(CIMA_E_INVALID, "%s: slab must be a non-null 256-byte aligned device pointer", api);
+    // slab layout: W as f16 [n, k] | X as f16 [m, k] (unless X is f16) | workspace
+    const size_t wbytes = align256((size_t)n * k * 2);
+    const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
+    // fused kernel up to two 128-token tiles; beyond, its per-tile weight
+    // decode costs more than one decode into the slab (14336x4096 Q4_K, bf16
+    // X, fp32 Y on MI355X: 80 against 76 us at m = 256, 116 against 80 at 384)
+    const int min_m = ctx->gemm_lib_min > 0 ? ctx->gemm_lib_min : 257;
+    if (m < min_m || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
+        return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
+    const size_t rest = (size_t)slab_bytes - wbytes - xbytes;
+    const size_t ws_cap = rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax;
+    LtPlan* p = nullptr;
+    if ((rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p))) return rc;
+    if (!p->ok) return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
+    uint8_t* base = static_cast<uint8_t*>(slab);
+    // W rows are whole blocks laid end to end: one flat run decodes to [n, k]
+    if ((rc = cima_hip_gguf_dequant(ctx, t, w, base, (long long)n * (k / F->block_elems)))) return rc;
+    const void* xh = x;
+    if (x_dtype != CIMA_DT_F16) {
+        hipFunction_t f;
+        if ((rc = get_fn(ctx, "cima_x_to_f16", &f))) return rc;
+        const void* src = x;
+        void* dst = base + wbytes;
+        long long n8 = (long long)m * k / 8;
+        int in_bf16 = x_dtype == CIMA_DT_BF16;
+        void* args[] = {&src, &dst, &n8, &in_bf16};
+        if ((rc = launch(ctx, f, (unsigned)((n8 + 255) / 256), 256, args, api))) return rc;
+        xh = dst;
+    }
+    const float alpha = 1.f, beta = 0.f;
+    const LtApi& L = lt_api();
+    hipblasStatus_t st = L.matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, base, p->a, xh, p->b, &beta, y, p->d,
+                                  y, p->d, &p->algo, p->ws ? base + wbytes + xbytes : nullptr, p->ws, ctx->stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);
+    ctx->last_gemm_route = 1;
+    return 0;
+}
+
+int cima_hip_set_gemm_route(cima_hip_ctx* ctx, int min_tokens) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemm_route: null context");
+    if (min_tokens < 0) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_route: %d < 0", min_tokens);
+    ctx->gemm_lib_min = min_tokens;
+    return 0;
+}
+
+int cima_hip_last_gemm_route(cima_hip_ctx* ctx) { return ctx ? ctx->last_gemm_route : -1; }
 
 int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int t, const void* src, void* out, long long nblocks) {
     if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_dequant: context is not initialised");

@@ -7,7 +7,9 @@
  * device pointers (hipMalloc'd or any HIP-visible device memory), sizes are
  * element or row counts, and every call is asynchronous on the context's
  * stream.  No call allocates device memory, so all are safe inside HIP
- * graph capture once the context exists.
+ * graph capture once the context exists -- except the first library-routed
+ * cima_hip_gguf_gemm_slab call of each shape, which creates hipBLASLt's
+ * handle and plan (make it once before capturing).
  *
  * Return value: 0 on success; a positive hipError_t when the HIP runtime
  * failed; a negative CIMA_E_* code when the arguments were rejected before
@@ -48,6 +50,7 @@ extern "C" {
 #define CIMA_E_FORMAT -2      /* not a supported GGUF block format */
 #define CIMA_E_NO_KERNEL -3   /* code object lacks the kernel */
 #define CIMA_E_NOT_INIT -4    /* null or destroyed context */
+#define CIMA_E_LIBRARY -5     /* hipBLASLt refused a call (cima_hip_gguf_gemm_slab) */
 
 typedef struct cima_hip_ctx cima_hip_ctx;
 
@@ -154,6 +157,34 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
  * Requires k % 64 == 0 (and k % 256 for K-quants), x 16-byte aligned. */
 int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                        int m, int n, int k, int ldy, int x_dtype, int y_dtype);
+
+/* Prefill GEMM through a dequant slab: the reference's lin_gemm / WTensor::
+ * gemm route (src/models/transformer.rs:618-655, src/quant.rs:120-129:
+ * gguf_dequant into the DQ_SCRATCH slab, then cublasGemmEx through
+ * gemm_dispatch, src/cuda.rs:2285-2320, 2468-2541), with hipBLASLt (opened
+ * with dlopen) as the library.  Same arguments and result as
+ * cima_hip_gguf_gemm, plus a caller-owned device slab (256-byte aligned):
+ *   [W as f16, n*k*2 B][X as f16, m*k*2 B unless x_dtype is f16][workspace]
+ * each part rounded up to 256 B; up to 32 MiB of the rest is the library's
+ * workspace.  W is decoded bit-exactly, X rounded to f16 as the fused
+ * kernel rounds it, the product accumulated in fp32.  Runs the fused kernel
+ * (cima_hip_gguf_gemm) instead when m is below the route threshold (257
+ * tokens; measured on MI355X, 14336x4096 Q4_K, bf16 X, fp32 Y: 90 us here
+ * against 122 us fused at m = 512, 76 against 80 at 256), when ldy != n,
+ * when the slab is too small or when hipBLASLt is absent or offers no
+ * algorithm; cima_hip_last_gemm_route() tells which ran.  The slab and
+ * the workspace are overwritten; calls sharing a slab must be ordered. */
+int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
+                            int m, int n, int k, int ldy, int x_dtype, int y_dtype, void* slab,
+                            unsigned long long slab_bytes);
+
+/* Route threshold of cima_hip_gguf_gemm_slab (no counterpart in the
+ * reference): the fewest tokens sent to the library GEMM; 0 = 257. */
+int cima_hip_set_gemm_route(cima_hip_ctx* ctx, int min_tokens);
+
+/* 1 if the last cima_hip_gguf_gemm_slab call on ctx ran dequant + library
+ * GEMM, 0 if it ran the fused kernel (-1 for a null context). */
+int cima_hip_last_gemm_route(cima_hip_ctx* ctx);
 
 /* Dequantise nblocks consecutive blocks to f16, bit-exact with the host
  * decoders: replaces CudaCtx::gguf_dequant (src/cuda.rs:2285-2320). */
