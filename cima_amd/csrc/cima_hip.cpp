@@ -756,6 +756,37 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, 
     return 0;
 }
 
+// rounds X (f32 or bf16, m*k elements, m*k % 8 == 0) to f16 at dst
+int x_to_f16(cima_hip_ctx* ctx, const void* x, void* dst, long long elems, int x_dtype, const char* api) {
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, "cima_x_to_f16", &f)) return rc;
+    const void* src = x;
+    long long n8 = elems / 8;
+    int in_bf16 = x_dtype == CIMA_DT_BF16;
+    void* args[] = {&src, &dst, &n8, &in_bf16};
+    return launch(ctx, f, (unsigned)((n8 + 255) / 256), 256, args, api);
+}
+
+// Y[m, n] (ld n) = Xh[m, k] . Wh[n, k]^T through hipBLASLt, f16 operands,
+// fp32 accumulation; *ran = false (nothing launched) when the library is
+// absent or has no algorithm for the shape within ws_cap bytes of workspace
+int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, int n, int k, int y_dtype, void* ws,
+            size_t ws_cap, const char* api, bool* ran) {
+    *ran = false;
+    if (!lt_api().ok) return 0;
+    LtPlan* p = nullptr;
+    if (int rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p)) return rc;
+    if (!p->ok) return 0;
+    const float alpha = 1.f, beta = 0.f;
+    hipblasStatus_t st = lt_api().matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y,
+                                         p->d, y, p->d, &p->algo, p->ws ? ws : nullptr, p->ws, ctx->stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);
+    *ran = true;
+    return 0;
+}
+
+size_t ws_cap_of(size_t rest) { return rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax; }
+
 }  // namespace
 
 int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
@@ -776,8 +807,9 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void*
     const int min_m = ctx->gemm_lib_min > 0 ? ctx->gemm_lib_min : 257;
     if (m < min_m || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
         return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
-    const size_t rest = (size_t)slab_bytes - wbytes - xbytes;
-    const size_t ws_cap = rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax;
+    // the library route is taken only if hipBLASLt has a plan for the shape:
+    // ask before decoding anything
+    const size_t ws_cap = ws_cap_of((size_t)slab_bytes - wbytes - xbytes);
     LtPlan* p = nullptr;
     if ((rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p))) return rc;
     if (!p->ok) return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
@@ -786,21 +818,12 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void*
     if ((rc = cima_hip_gguf_dequant(ctx, t, w, base, (long long)n * (k / F->block_elems)))) return rc;
     const void* xh = x;
     if (x_dtype != CIMA_DT_F16) {
-        hipFunction_t f;
-        if ((rc = get_fn(ctx, "cima_x_to_f16", &f))) return rc;
-        const void* src = x;
-        void* dst = base + wbytes;
-        long long n8 = (long long)m * k / 8;
-        int in_bf16 = x_dtype == CIMA_DT_BF16;
-        void* args[] = {&src, &dst, &n8, &in_bf16};
-        if ((rc = launch(ctx, f, (unsigned)((n8 + 255) / 256), 256, args, api))) return rc;
-        xh = dst;
+        if ((rc = x_to_f16(ctx, x, base + wbytes, (long long)m * k, x_dtype, api))) return rc;
+        xh = base + wbytes;
     }
-    const float alpha = 1.f, beta = 0.f;
-    const LtApi& L = lt_api();
-    hipblasStatus_t st = L.matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, base, p->a, xh, p->b, &beta, y, p->d,
-                                  y, p->d, &p->algo, p->ws ? base + wbytes + xbytes : nullptr, p->ws, ctx->stream);
-    if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);
+    bool ran = false;
+    if ((rc = lt_gemm(ctx, base, xh, y, m, n, k, y_dtype, base + wbytes + xbytes, ws_cap, api, &ran))) return rc;
+    if (!ran) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt plan vanished", api);
     ctx->last_gemm_route = 1;
     return 0;
 }
@@ -1276,4 +1299,41 @@ int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, cons
     snprintf(name, sizeof name, "cima_nf4_gemv_e_%s_%s", an, an);
     void* args[] = {&xp, &pk, &am, &qm, &yp, &nn, &kk, &bs};
     return launch_named(ctx, name, (unsigned)((n + 3) / 4), 256, args, api);
+}
+
+int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax,
+                           const float* qmap, void* y, int m, int n, int k, int blocksize, int x_dtype, int y_dtype,
+                           void* slab, unsigned long long slab_bytes) {
+    const char* api = "cima_hip_nf4_gemm_slab";
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    if (m < 0 || n < 0 || k <= 0 || k % 8 || blocksize <= 0)
+        return fail(CIMA_E_INVALID, "%s: m=%d n=%d k=%d blocksize=%d (k must be a positive multiple of 8)", api, m, n,
+                    k, blocksize);
+    if (x_dtype < CIMA_DT_F32 || x_dtype > CIMA_DT_BF16 || (y_dtype != CIMA_DT_F32 && y_dtype != CIMA_DT_F16))
+        return fail(CIMA_E_INVALID, "%s: x_dtype %d / y_dtype %d not supported", api, x_dtype, y_dtype);
+    if (m == 0 || n == 0) return 0;
+    if (!x || !packed || !absmax || !qmap || !y || !slab) return fail(CIMA_E_INVALID, "%s: null pointer", api);
+    if (!aligned(x, 16) || !aligned(y, 4) || !aligned(slab, 256))
+        return fail(CIMA_E_INVALID, "%s: misaligned x (16 B), y (4 B) or slab (256 B)", api);
+    const size_t wbytes = align256((size_t)n * k * 2);
+    const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
+    if (slab_bytes < wbytes + xbytes)
+        return fail(CIMA_E_INVALID, "%s: slab of %llu bytes is smaller than the %zu the f16 W and X need", api,
+                    slab_bytes, wbytes + xbytes);
+    if (!lt_api().ok) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt (libhipblaslt.so.1) could not be opened", api);
+    const size_t ws_cap = ws_cap_of((size_t)slab_bytes - wbytes - xbytes);
+    LtPlan* p = nullptr;
+    int rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p);
+    if (rc) return rc;
+    if (!p->ok) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt offers no algorithm for m=%d n=%d k=%d", api, m, n, k);
+    uint8_t* base = static_cast<uint8_t*>(slab);
+    if ((rc = cima_hip_nf4_dequant(ctx, packed, absmax, qmap, base, (long long)n * k, blocksize))) return rc;
+    const void* xh = x;
+    if (x_dtype != CIMA_DT_F16) {
+        if ((rc = x_to_f16(ctx, x, base + wbytes, (long long)m * k, x_dtype, api))) return rc;
+        xh = base + wbytes;
+    }
+    bool ran = false;
+    if ((rc = lt_gemm(ctx, base, xh, y, m, n, k, y_dtype, base + wbytes + xbytes, ws_cap, api, &ran))) return rc;
+    return ran ? 0 : fail(CIMA_E_LIBRARY, "%s: hipBLASLt plan vanished", api);
 }

@@ -42,7 +42,7 @@ EXPORTS = (
     "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
     "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
-    "cima_hip_nf4_dequant", "cima_hip_nf4_gemv", "cima_hip_set_nf4_tuning",
+    "cima_hip_nf4_dequant", "cima_hip_nf4_gemv", "cima_hip_set_nf4_tuning", "cima_hip_nf4_gemm_slab",
     "cima_hip_stream_read",
 )
 
@@ -124,6 +124,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_nf4_dequant.argtypes = [P, P, P, P, P, LL, I]
     L.cima_hip_nf4_gemv.argtypes = [P, P, P, P, P, P, I, I, I, I]
     L.cima_hip_set_nf4_tuning.argtypes = [P, I, I]
+    L.cima_hip_nf4_gemm_slab.argtypes = [P, P, P, P, P, P, I, I, I, I, I, I, P, ctypes.c_ulonglong]
     L.cima_hip_capture_end.argtypes = [P, ctypes.POINTER(P)]
     L.cima_hip_graph_launch.argtypes = [P, P]
     L.cima_hip_graph_destroy.argtypes = [P]
@@ -318,6 +319,18 @@ class HipCtx:
             act_dtype = _act_of(x) if hasattr(x, "dtype") else gguf.DT_F16
         self._check(self.lib.cima_hip_nf4_gemv(self.handle, _ptr(x), _ptr(packed), _ptr(absmax), _ptr(qmap), _ptr(y),
                                                n, k, blocksize, act_dtype))
+
+    def nf4_gemm_slab(self, x, packed, absmax, qmap, y, m: int, n: int, k: int, blocksize: int, slab,
+                      slab_bytes: Optional[int] = None, x_dtype: Optional[int] = None,
+                      y_dtype: Optional[int] = None) -> None:
+        """WTensor::gemm for an NF4 weight (src/quant.rs:131-162): ``Y[m, n] = X . W^T``,
+        W decoded into the f16 ``slab`` and multiplied by hipBLASLt."""
+        xd, yd = self._gemm_dtypes(x, y, x_dtype, y_dtype)
+        if slab_bytes is None:
+            slab_bytes = slab.numel() * slab.element_size()
+        self._check(self.lib.cima_hip_nf4_gemm_slab(self.handle, _ptr(x), _ptr(packed), _ptr(absmax), _ptr(qmap),
+                                                    _ptr(y), m, n, k, blocksize, xd, yd, _ptr(slab),
+                                                    int(slab_bytes)))
 
     def set_nf4_tuning(self, rows: int = 0, kernel: int = 0) -> None:
         """Fast NF4 GEMV: rows per wave (1, 2, 4) and kernel (1 = LDS pair table,

@@ -251,10 +251,9 @@ class Nf4Weight:
 
     def gemm(self, ctx, x, y, scratch=None) -> None:
         """WTensor::gemm for a packed weight (src/quant.rs:131-162): y[m, n] = x[m, k] . W^T.
-        m == 1 runs the fused GEMV; m > 1 dequantises into ``scratch``
-        (rows*cols f16) and multiplies with the library GEMM."""
-        import torch
-
+        m == 1 runs the fused GEMV; m > 1 dequantises into the ``scratch``
+        slab and multiplies with the library GEMM (cima_hip_nf4_gemm_slab);
+        ``HipCtx.gemm_slab_bytes(m, n, k)`` bytes are enough."""
         m = x.shape[0] if x.dim() == 2 else 1
         n, k = y.shape[-1], x.shape[-1]
         self._check_shape(n, k)
@@ -263,9 +262,4 @@ class Nf4Weight:
             return
         if scratch is None:
             raise _err("nf4 prefill GEMM requires a dequant scratch buffer")
-        if scratch.numel() < n * k or scratch.dtype != torch.float16:
-            raise _err(f"nf4 prefill scratch must hold {n * k} f16 elements")
-        self.dequant(ctx, scratch)
-        ctx.sync()  # the dequant ran on the context's stream; the GEMM runs on torch's
-        w = scratch[: n * k].reshape(n, k)
-        y.copy_(torch.matmul(x.to(torch.float16), w.t()))
+        ctx.nf4_gemm_slab(x, self.packed, self.absmax, self.qmap, y, m, n, k, self.blocksize, scratch)

@@ -50,7 +50,7 @@ extern "C" {
 #define CIMA_E_FORMAT -2      /* not a supported GGUF block format */
 #define CIMA_E_NO_KERNEL -3   /* code object lacks the kernel */
 #define CIMA_E_NOT_INIT -4    /* null or destroyed context */
-#define CIMA_E_LIBRARY -5     /* hipBLASLt refused a call (cima_hip_gguf_gemm_slab) */
+#define CIMA_E_LIBRARY -5     /* hipBLASLt absent or refused a call (the *_gemm_slab entry points) */
 
 typedef struct cima_hip_ctx cima_hip_ctx;
 
@@ -367,6 +367,17 @@ int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, cons
  * heuristic, 1 = LDS pair table, 2 = codebook in registers).  The grid
  * width follows cima_hip_set_gemv_grid. */
 int cima_hip_set_nf4_tuning(cima_hip_ctx* ctx, int rows, int kernel);
+/* Prefill GEMM over the packed weight, Y[m, n] (row stride n) = X[m, k] .
+ * W[n, k]^T: WTensor::gemm's Nf4 arm (src/quant.rs:131-162), which runs
+ * nf4_dequant into the engine's slab, then gemm_f16.  Here W is decoded
+ * bit-exactly (cima_hip_nf4_dequant) into the caller's 256-byte aligned
+ * slab, X (f32 / bf16) rounded to f16 behind it, and hipBLASLt multiplies
+ * them with fp32 accumulation; slab layout as cima_hip_gguf_gemm_slab.
+ * k % 8 == 0, x 16-byte aligned.  CIMA_E_LIBRARY if hipBLASLt is absent or
+ * has no algorithm for the shape. */
+int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax,
+                           const float* qmap, void* y, int m, int n, int k, int blocksize, int x_dtype,
+                           int y_dtype, void* slab, unsigned long long slab_bytes);
 
 /* Bandwidth reference (no counterpart in the reference): reads nbytes
  * (16-byte aligned src, whole 16-byte words) once with plain streaming

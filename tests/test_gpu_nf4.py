@@ -166,7 +166,7 @@ def test_gemv_double_quantised_from_safetensors(hip, tmp_path):
     m = 5
     xs = torch.randn(m, k, device="cuda", dtype=torch.float16)
     ys = torch.empty(m, n, device="cuda", dtype=torch.float16)
-    scratch = torch.empty(n * k, device="cuda", dtype=torch.float16)
+    scratch = torch.empty(hip.gemm_slab_bytes(m, n, k, x_f16=True), device="cuda", dtype=torch.uint8)
     wt.gemm(hip, xs, ys, scratch)
     torch.cuda.synchronize()
     w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(h.packed, h.absmax, h.qmap, n * k, bs)).reshape(n, k)
@@ -220,3 +220,46 @@ def test_gemv_many_rows_per_wave(hip, rows, kernel):
     assert not np.isnan(got).any()
     want = oracle.nf4_gemv(packed, absmax, qmap, x.astype(np.float32), n, k, bs, threads=8)
     assert rel(got, want) < 1e-3
+
+
+TDT = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
+
+
+@pytest.mark.parametrize("m, n, k, bs", [(2, 256, 512, 64), (17, 320, 1024, 128), (300, 512, 2048, 64),
+                                         (9, 130, 200, 20)])
+def test_gemm_slab_parity(hip, m, n, k, bs):
+    """cima_hip_nf4_gemm_slab (WTensor::gemm's Nf4 arm, src/quant.rs:131-162)
+    against the CPU path: the oracle's bit-exact f16 W times the f16-rounded X
+    in float64; 1e-5 with fp32 Y (only the summation order differs), the
+    north star's 1e-3 with f16 Y."""
+    packed, absmax, qmap = case(700 + m, n * k, bs, code=RANDOM_CODE)
+    w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(packed, absmax, qmap, n * k, bs)).reshape(n, k)
+    xf = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    p, a, q = dev(packed), dev(absmax), dev(qmap)
+    for xd, yd in ((2, 0), (1, 1), (0, 0)):
+        x = torch.from_numpy(xf).to(TDT[xd]).cuda()
+        y = torch.full((m, n), 3.0, dtype=TDT[yd], device="cuda")
+        slab = torch.empty(hip.gemm_slab_bytes(m, n, k, x_f16=xd == 1), dtype=torch.uint8, device="cuda")
+        hip.nf4_gemm_slab(x, p, a, q, y, m, n, k, bs, slab)
+        torch.cuda.synchronize()
+        xh = x.float().cpu().numpy().astype(np.float16).astype(np.float64)
+        r = rel(y.float().cpu().numpy(), xh @ w16.astype(np.float64).T)
+        assert r <= (1e-5 if yd == 0 else 1e-3), (xd, yd, r)
+
+
+def test_gemm_slab_argument_errors(hip):
+    m, n, k, bs = 4, 64, 256, 64
+    packed, absmax, qmap = case(5, n * k, bs)
+    p, a, q = dev(packed), dev(absmax), dev(qmap)
+    x = torch.zeros((m, k), dtype=torch.float16, device="cuda")
+    y = torch.zeros((m, n), dtype=torch.float16, device="cuda")
+    slab = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
+    hip.nf4_gemm_slab(x, p, a, q, y, 0, n, k, bs, slab)  # m = 0: no-op
+    for bad in (dict(slab_bytes=2 * n * k - 1), dict(k=100)):
+        kk = bad.get("k", k)
+        with pytest.raises(EngineError) as e:
+            hip.nf4_gemm_slab(x, p, a, q, y, m, n, kk, bs, slab, slab_bytes=bad.get("slab_bytes"))
+        assert e.value.code == E_INVALID
+    with pytest.raises(EngineError) as e:
+        hip.nf4_gemm_slab(x, p, a, q, y, m, n, k, bs, slab[64:])
+    assert e.value.code == E_INVALID
