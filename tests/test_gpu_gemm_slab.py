@@ -156,3 +156,36 @@ def test_slab_argument_errors(hip):
     with pytest.raises(EngineError) as e:
         hip.set_gemm_route(-1)
     assert e.value.code == E_INVALID
+
+
+def test_slab_route_graph_replay(hip):
+    """After a first (plan-making) call, the library route captured into a
+    HIP graph replays to the eager result every time, with eager work
+    between the replays (a library that recorded a memset node would show
+    here)."""
+    n, k, m = 2048, 1024, 300
+    w = torch.from_numpy(synth.weights(Q4_K, 120, 0.02, n, k)).cuda()
+    x = torch.from_numpy(synth.normal(121, 1.0, m * k).reshape(m, k)).to(torch.bfloat16).cuda()
+    slab = slab_for(m, n, k, gguf.DT_BF16)
+    y = torch.empty((m, n), device="cuda")
+    assert hip.gguf_gemm_slab(Q4_K, x, w, y, m, n, k, slab) == 1
+    torch.cuda.synchronize()
+    eager = y.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    yg = torch.zeros((m, n), device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            hip.set_stream(s.cuda_stream)
+            hip.gguf_gemm_slab(Q4_K, x, w, yg, m, n, k, slab)
+    hip.use_torch_stream()
+    torch.cuda.synchronize()
+    for i in range(4):
+        yg.zero_()
+        slab.fill_(0xFF)  # the replay must rebuild the slab itself
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(yg.cpu().numpy(), eager), i
+        hip.gguf_gemm_slab(Q4_K, x, w, y, m, n, k, slab)  # eager work between replays
+        torch.cuda.synchronize()
