@@ -121,6 +121,7 @@ struct cima_hip_ctx {
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
     int gemm_lib_min = 0;     // dequant-slab prefill: fewest tokens routed to the library GEMM (0 = 257)
     int last_gemm_route = 0;  // route of the last gguf_gemm_slab call: 0 fused MFMA kernel, 1 slab + library
+    int gemm_autotune = 0;    // time hipBLASLt's candidates on a shape's first library call
     void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
     // cached library plans: (m, n, k, y dtype, workspace cap) -> plan
     std::map<std::tuple<int, int, int, int, size_t>, struct LtPlan*> lt_plans;
@@ -224,6 +225,13 @@ struct LtPlan {
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
     hipblasLtMatmulAlgo_t algo;
     size_t ws = 0;
+    // the heuristic's candidates (best-ranked first) and whether they have
+    // been timed on the device (autotuning)
+    static constexpr int kMaxCand = 8;
+    hipblasLtMatmulAlgo_t cand[kMaxCand];
+    size_t cand_ws[kMaxCand] = {};
+    int ncand = 0;
+    bool tuned = false;
 };
 
 namespace {
@@ -506,6 +514,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
+    if (const char* s = getenv("CIMA_GEMM_AUTOTUNE")) ctx->gemm_autotune = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -738,22 +747,67 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, 
     if (ok) {
         hipblasLtMatmulPreference_t pref = nullptr;
         uint64_t cap = ws_cap;
-        hipblasLtMatmulHeuristicResult_t res[1];
+        hipblasLtMatmulHeuristicResult_t res[LtPlan::kMaxCand];
         int found = 0;
         ok = L.pref_create(&pref) == HIPBLAS_STATUS_SUCCESS &&
              L.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof cap) == HIPBLAS_STATUS_SUCCESS &&
-             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, 1, res, &found) ==
-                 HIPBLAS_STATUS_SUCCESS &&
-             found > 0 && res[0].workspaceSize <= ws_cap;
+             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, LtPlan::kMaxCand, res,
+                         &found) == HIPBLAS_STATUS_SUCCESS;
         if (pref) (void)L.pref_destroy(pref);
+        for (int i = 0; ok && i < found && i < LtPlan::kMaxCand; i++)
+            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_cap) {
+                p->cand[p->ncand] = res[i].algo;
+                p->cand_ws[p->ncand++] = res[i].workspaceSize;
+            }
+        ok = ok && p->ncand > 0;
         if (ok) {
-            p->algo = res[0].algo;
-            p->ws = res[0].workspaceSize;
+            p->algo = p->cand[0];
+            p->ws = p->cand_ws[0];
         }
     }
     p->ok = ok;
     *out = p;
     return 0;
+}
+
+// Times each heuristic candidate of the plan on the call's own operands
+// (one warm-up and three timed runs, HIP events on the context stream; the
+// host waits) and keeps the fastest.  y receives results that the call's
+// own GEMM then overwrites.  Skipped while the stream is being captured.
+void lt_autotune(cima_hip_ctx* ctx, LtPlan* p, const void* wh, const void* xh, void* y, void* ws) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    p->tuned = true;
+    if (p->ncand < 2) return;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        if (e0) (void)hipEventDestroy(e0);
+        return;
+    }
+    const LtApi& L = lt_api();
+    const float alpha = 1.f, beta = 0.f;
+    float best = 0.f;
+    int best_i = 0;
+    for (int i = 0; i < p->ncand; i++) {
+        auto run = [&] {
+            return L.matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y, p->d, y, p->d,
+                            &p->cand[i], p->cand_ws[i] ? ws : nullptr, p->cand_ws[i], ctx->stream) ==
+                   HIPBLAS_STATUS_SUCCESS;
+        };
+        bool ok = run() && hipEventRecord(e0, ctx->stream) == hipSuccess;
+        for (int r = 0; ok && r < 3; r++) ok = run();
+        float ms = 0.f;
+        ok = ok && hipEventRecord(e1, ctx->stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
+             hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+        if (ok && (i == 0 || ms < best || best == 0.f)) {
+            best = ms;
+            best_i = i;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    p->algo = p->cand[best_i];
+    p->ws = p->cand_ws[best_i];
 }
 
 // rounds X (f32 or bf16, m*k elements, m*k % 8 == 0) to f16 at dst
@@ -778,6 +832,7 @@ int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, i
     if (int rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p)) return rc;
     if (!p->ok) return 0;
     const float alpha = 1.f, beta = 0.f;
+    if (ctx->gemm_autotune && !p->tuned) lt_autotune(ctx, p, wh, xh, y, ws);
     hipblasStatus_t st = lt_api().matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y,
                                          p->d, y, p->d, &p->algo, p->ws ? ws : nullptr, p->ws, ctx->stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);

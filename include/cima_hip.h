@@ -172,7 +172,9 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const vo
  * tokens; measured on MI355X, 14336x4096 Q4_K, bf16 X, fp32 Y: 90 us here
  * against 122 us fused at m = 512, 76 against 80 at 256), when ldy != n,
  * when the slab is too small or when hipBLASLt is absent or offers no
- * algorithm; cima_hip_last_gemm_route() tells which ran.  The slab and
+ * algorithm; cima_hip_last_gemm_route() tells which ran.  With the
+ * environment variable CIMA_GEMM_AUTOTUNE=1 at cima_hip_init, the first
+ * library call of each shape times hipBLASLt's candidates (host waits).  The slab and
  * the workspace are overwritten; calls sharing a slab must be ordered. */
 int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                             int m, int n, int k, int ldy, int x_dtype, int y_dtype, void* slab,

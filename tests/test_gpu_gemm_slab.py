@@ -189,3 +189,20 @@ def test_slab_route_graph_replay(hip):
         assert np.array_equal(yg.cpu().numpy(), eager), i
         hip.gguf_gemm_slab(Q4_K, x, w, y, m, n, k, slab)  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_slab_route_autotuned(monkeypatch):
+    """CIMA_GEMM_AUTOTUNE=1 (read by the context at init): hipBLASLt's
+    candidates are timed on the first call of a shape; every later result
+    still matches the CPU path."""
+    monkeypatch.setenv("CIMA_GEMM_AUTOTUNE", "1")
+    ctx = HipCtx(0)
+    ctx.use_torch_stream()
+    n, k, m = 512, 1024, 300
+    w = synth.weights(Q4_K, 130, 0.02, n, k)
+    xf = synth.normal(131, 1.0, m * k).reshape(m, k)
+    w16 = oracle.dequant(Q4_K, w, n * k)
+    for _ in range(2):
+        y, xh, route = run_slab(ctx, Q4_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
+        assert route == 1
+        assert rel(y, oracle.gemm(xh, w16, m, n, k)) <= 1e-5
