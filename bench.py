@@ -240,8 +240,8 @@ def main():
         # config 4: prefill dequant-GEMM on MFMA, Q4_K 14336x4096, X bf16 (m tokens), Y fp32
         gw = synth.weights(Q4_K, 300, 0.02, FFN, HID)
         gbufs = [torch.from_numpy(gw).to(dev) for _ in range(12)]
-        # the prefill route of the engine: fused MFMA kernel up to 256 tokens,
-        # dequant into this slab + hipBLASLt beyond (cima_hip_gguf_gemm_slab)
+        # the prefill route of the engine (cima_hip_gguf_gemm_slab): fused MFMA
+        # kernel or dequant into this slab + hipBLASLt, whichever its rule picks
         gslab = torch.empty(ctx.gemm_slab_bytes(512, FFN, HID), dtype=torch.uint8, device=dev)
         for m in (16, 128, 512):
             gx = torch.from_numpy(synth.normal(301, 1.0, m * HID)).to(dev).to(torch.bfloat16).reshape(m, HID)

@@ -119,7 +119,7 @@ struct cima_hip_ctx {
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
-    int gemm_lib_min = 0;     // dequant-slab prefill: fewest tokens routed to the library GEMM (0 = 257)
+    int gemm_lib_min = 0;     // dequant-slab prefill: fewest tokens routed to the library GEMM (0 = built-in rule)
     int last_gemm_route = 0;  // route of the last gguf_gemm_slab call: 0 fused MFMA kernel, 1 slab + library
     int gemm_autotune = 0;    // time hipBLASLt's candidates on a shape's first library call
     void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
@@ -679,12 +679,12 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     // token tile (measured on MI355X, 14336x4096 Q4_K): 16 up to 32 tokens
     // (two 16-token tiles at 33.6 us against 40.2 us for one 64-token tile),
     // 64 up to 128 (twice the workgroups of 128-token tiles), 128 beyond;
-    // the 16-token tile stages 128 k at a time (64-row weight tiles in
-    // 1024-thread workgroups), so it needs k % 128 == 0
+    // the 16-token tile stages 128 k at a time (32-row weight tiles in
+    // 512-thread workgroups), so it needs k % 128 == 0
     int bn = m <= 32 ? 16 : (m <= 128 ? 64 : 128);
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
     if (bn == 16 && k % 128) bn = 64;
-    const int bm = bn == 16 ? 64 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)
+    const int bm = bn == 16 ? 32 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];
     snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xn[x_dtype], y_dtype == CIMA_DT_F32 ? "f32" : "f16");
@@ -695,7 +695,7 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     void* ya = y;
     int mm = m, nn = n, kk = k, ld = ldy;
     void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
-    const unsigned threads = bn == 16 ? 1024 : 256;
+    const unsigned threads = bn == 16 ? 512 : 256;
     hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, threads, 1,
                                          1, 0, ctx->stream, args, nullptr);
     return e == hipSuccess ? 0 : hip_fail(e, api);
@@ -840,6 +840,25 @@ int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, i
     return 0;
 }
 
+// Built-in route of cima_hip_gguf_gemm_slab.  Measured on MI355X (Q4_K,
+// bf16 X, fp32 Y, cold weights; fused / slab + hipBLASLt in us):
+//   14336x4096  m=16 18/54   m=64 42/56   m=128 44/62   m=256 70/76  m=384 107/79
+//   4096x14336  m=16 42/54   m=48 128/62  m=128 129/93  m=256 205/90
+//   4096x4096   m=16 13/32   m=48 39/34   m=192 64/47   m=256 64/38
+//   1024x4096   m=16 13/19   m=48 38/19   m=256 64/25
+//   6144x4096   m=48 39/39   m=128 40/45  m=192 65/50
+// The split-k 16-token tiles win up to 32 tokens everywhere.  The 64- and
+// 128-token tiles give one workgroup per 128 weight rows and token tile, and
+// a narrow grid of long rows leaves most CUs idle: the slab route wins
+// there, and past 256 tokens, where the per-tile weight decode dominates.
+bool slab_route_pays(int m, int n, int k) {
+    if (m <= 32) return false;
+    if (m > 256) return true;
+    const int bn = m <= 128 ? 64 : 128;
+    const long long wgs = (long long)((n + 127) / 128) * ((m + bn - 1) / bn);
+    return wgs * 4096 < (long long)(bn == 64 ? 48 : 160) * k;
+}
+
 size_t ws_cap_of(size_t rest) { return rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax; }
 
 }  // namespace
@@ -856,11 +875,8 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void*
     // slab layout: W as f16 [n, k] | X as f16 [m, k] (unless X is f16) | workspace
     const size_t wbytes = align256((size_t)n * k * 2);
     const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
-    // fused kernel up to two 128-token tiles; beyond, its per-tile weight
-    // decode costs more than one decode into the slab (14336x4096 Q4_K, bf16
-    // X, fp32 Y on MI355X: 80 against 76 us at m = 256, 116 against 80 at 384)
-    const int min_m = ctx->gemm_lib_min > 0 ? ctx->gemm_lib_min : 257;
-    if (m < min_m || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
+    const bool lib = ctx->gemm_lib_min > 0 ? m >= ctx->gemm_lib_min : slab_route_pays(m, n, k);
+    if (!lib || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
         return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
     // the library route is taken only if hipBLASLt has a plan for the shape:
     // ask before decoding anything

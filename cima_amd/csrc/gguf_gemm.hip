@@ -265,12 +265,14 @@ struct XTile {
     }
 };
 
-// Tile shapes.  BN = 16 (up to 16 tokens): gemm_body_sk16, 64 rows per
-// 1024-thread workgroup, so a 14336-row weight spreads over 224
-// workgroups of 16 waves (measured on MI355X, 14336x4096 Q4_K, bf16 X:
-// 18.6 us at m = 16 against 23.0 us for 64-row tiles of 4 waves staging
-// the weights through LDS; deeper rings, x held whole in LDS, or 8 and 4
-// waves per workgroup were slower).  BN = 64: gemm_body_ra,
+// Tile shapes.  BN = 16 (up to 16 tokens): gemm_body_sk16, 32 rows per
+// 512-thread workgroup (RT = 2 row tiles x 4 k-splits, one stage in
+// flight), so a 14336-row weight spreads over 448 workgroups of 8 waves,
+// two per CU (measured on MI355X, Q4_K, bf16 X, m = 16, cold weights:
+// 18.4 / 42.7 / 12.7 us for 14336x4096 / 4096x14336 / 4096x4096 against
+// 19.8 / 47.8 / 16.6 us for 64-row tiles of 16 waves with two stages in
+// flight, 25 us with 16-row tiles; 64-row tiles of 4 waves staging the
+// weights through LDS took 23.0 us on 14336x4096).  BN = 64: gemm_body_ra,
 // 128 rows (32 per wave) x 64 k per stage, weights dequantised straight
 // into the MFMA operand registers.  BN = 128: gemm_body_wide, 128 x 64
 // stages through LDS on a 2 x 2 wave grid.  PF stages of weights and
@@ -281,7 +283,6 @@ struct XTile {
 // through LDS; at m = 256 / 512 the LDS-staged 2 x 2 grid is faster (68 /
 // 105 us against 72 / 112).
 template <int BN> struct GemmTile;
-template <> struct GemmTile<16> { static constexpr int BM = 64, PF = 8; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
 
@@ -400,16 +401,15 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
     }
 }
 
-// Split-k tiles for up to 16 tokens: a 1024-thread workgroup owns 64
-// weight rows x 16 tokens; wave w takes the 16-row tile w % 4 and the
-// k-split w / 4, whose 128-k stages are s = w / 4, w / 4 + 4, ...  Lane l
+// Split-k tiles for up to 16 tokens: a workgroup of 4 RT waves owns 16 RT
+// weight rows x 16 tokens; wave w takes the 16-row tile w % RT and the
+// k-split w / RT, whose 128-k stages are s = w / RT, w / RT + 4, ...  Lane l
 // takes row l % 16 of its tile and dequantises sub-block g = l / 16 of the
 // stage straight into its A operand registers; v_mfma_f32_16x16x32_f16
 // step q uses elements [8q, 8q+8) of it, so its B fragment is x[32g + 8q,
 // +8) of token l % 16, read from the split's activation tile in LDS (the
-// split's four waves stage it together).  Sixteen waves per CU keep the
-// weight stream of a 224-workgroup grid in flight; the four splits' partial
-// tiles are summed through LDS at the end.
+// split's RT waves stage it together).  The four splits' partial tiles are
+// summed through LDS at the end.
 template <typename D, int XT, int YT, int PF, int RT>
 __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
                                int m, int n, int k, int ldy) {
@@ -616,13 +616,6 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
     }
 }
 
-// Stages in flight for gemm_body_sk16 (128 registers per thread): two
-// where a stage (raw sub-block + the lane's activation words) takes at most
-// 16 registers, else one
-template <typename D, int XT>
-constexpr int sk16_pf() {
-    return (int)(sizeof(typename D::Raw) / 4) + (XT == XT_F32 ? 8 : 4) <= 16 ? 2 : 1;
-}
 
 // Stages in flight for gemm_body_ra: GemmTile<BN>::PF, fewer where a stage
 // (the raw weight sub-block plus the thread's activation words) is so large
@@ -640,10 +633,10 @@ constexpr int ra_pf() {
 
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(BN == 16 ? 1024 : 256, BN == 16 ? 1 : 2) void           \
+    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, 2) void                          \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
-        if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, sk16_pf<D, XT>(), 4>(x, w, y, m, n, k, ldy); \
+        if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
         else if constexpr (BN == 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
         else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
     }

@@ -275,7 +275,7 @@ class HipCtx:
                        ldy: Optional[int] = None, x_dtype: Optional[int] = None,
                        y_dtype: Optional[int] = None) -> int:
         """The same product through the reference's prefill route: from
-        ``set_gemm_route`` tokens up (257 by default) W is decoded into the
+        ``set_gemm_route`` tokens up (by default where the built-in rule finds it faster) W is decoded into the
         f16 ``slab`` and multiplied by the library GEMM; fewer tokens run the
         fused kernel.  Returns the route taken (0 fused, 1 slab + library)."""
         xd, yd = self._gemm_dtypes(x, y, x_dtype, y_dtype)
@@ -287,7 +287,7 @@ class HipCtx:
         return int(self.lib.cima_hip_last_gemm_route(self.handle))
 
     def set_gemm_route(self, min_tokens: int = 0) -> None:
-        """Fewest tokens ``gguf_gemm_slab`` sends to the library GEMM (0 = 257)."""
+        """Fewest tokens ``gguf_gemm_slab`` sends to the library GEMM (0 = built-in rule)."""
         self._check(self.lib.cima_hip_set_gemm_route(self.handle, int(min_tokens)))
 
     @staticmethod

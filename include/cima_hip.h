@@ -168,9 +168,9 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const vo
  * each part rounded up to 256 B; up to 32 MiB of the rest is the library's
  * workspace.  W is decoded bit-exactly, X rounded to f16 as the fused
  * kernel rounds it, the product accumulated in fp32.  Runs the fused kernel
- * (cima_hip_gguf_gemm) instead when m is below the route threshold (257
- * tokens; measured on MI355X, 14336x4096 Q4_K, bf16 X, fp32 Y: 90 us here
- * against 122 us fused at m = 512, 76 against 80 at 256), when ldy != n,
+ * (cima_hip_gguf_gemm) instead where that is faster (built-in rule from
+ * MI355X measurements: up to 32 tokens always; 33-256 tokens unless the
+ * fused grid is narrow for the row length; never past 256), when ldy != n,
  * when the slab is too small or when hipBLASLt is absent or offers no
  * algorithm; cima_hip_last_gemm_route() tells which ran.  With the
  * environment variable CIMA_GEMM_AUTOTUNE=1 at cima_hip_init, the first
@@ -181,7 +181,8 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int ggml_type, const void* x, con
                             unsigned long long slab_bytes);
 
 /* Route threshold of cima_hip_gguf_gemm_slab (no counterpart in the
- * reference): the fewest tokens sent to the library GEMM; 0 = 257. */
+ * reference): the fewest tokens sent to the library GEMM; 0 = the
+ * built-in rule. */
 int cima_hip_set_gemm_route(cima_hip_ctx* ctx, int min_tokens);
 
 /* 1 if the last cima_hip_gguf_gemm_slab call on ctx ran dequant + library

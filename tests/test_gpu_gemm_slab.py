@@ -109,16 +109,26 @@ def test_slab_fused_fallbacks(route_all):
     assert route == 1 and rel(y, want) <= 1e-5
 
 
-def test_slab_default_threshold(hip):
-    """Built-in route: the fused kernel up to 256 tokens, the library beyond."""
-    n, k = 64, 256
+@pytest.mark.parametrize("n, k, m, want_route", [
+    (1024, 4096, 32, 0),    # split-k 16-token tiles: always fused
+    (1024, 4096, 33, 1),    # 8 workgroups of 64-token tiles: narrow grid
+    (14336, 1024, 128, 0),  # 112 workgroups of rows 1024 long
+    (14336, 1024, 129, 0),  # 224 workgroups of 128-token tiles, rows 1024 long
+    (4096, 4096, 129, 1),   # 64 workgroups of 128-token tiles, rows 4096 long
+    (256, 256, 256, 1),     # narrow grid
+    (14336, 256, 256, 0),
+    (14336, 256, 257, 1),   # past 256 tokens: always the slab
+])
+def test_slab_builtin_route(hip, n, k, m, want_route):
+    """The built-in route (slab_route_pays in cima_hip.cpp), and both
+    routes' results against the CPU path on 64 sampled rows."""
     w = synth.weights(Q5_K, 95, 0.02, n, k)
-    w16 = oracle.dequant(Q5_K, w, n * k)
-    for m, want_route in ((256, 0), (257, 1)):
-        xf = synth.normal(96 + m, 1.0, m * k).reshape(m, k)
-        y, xh, route = run_slab(hip, Q5_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
-        assert route == want_route, m
-        assert rel(y, oracle.gemm(xh, w16, m, n, k)) <= 1e-5
+    xf = synth.normal(96 + m, 1.0, m * k).reshape(m, k)
+    y, xh, route = run_slab(hip, Q5_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
+    assert route == want_route
+    rows = np.random.default_rng(n + m).choice(n, 64, replace=False)
+    w16 = oracle.dequant(Q5_K, np.stack([w[r] for r in rows]).reshape(-1), 64 * k)
+    assert rel(y[:, rows], oracle.gemm(xh, w16, m, 64, k)) <= 1e-5
 
 
 def test_slab_repeat_and_shape_change(route_all):
