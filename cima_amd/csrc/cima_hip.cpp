@@ -81,7 +81,7 @@ const Fmt* fmt_of(int t) {
 const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_1, CIMA_GGML_Q5_0, CIMA_GGML_Q5_1,
                         CIMA_GGML_Q4_K, CIMA_GGML_Q5_K, CIMA_GGML_Q6_K, CIMA_GGML_IQ4_XS};
 // prefill GEMM token-tile widths the code object is built for
-const int kGemmBN[] = {16, 64, 128};
+const int kGemmBN[] = {16, 32, 64, 128};
 
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
@@ -595,7 +595,7 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens) {
     if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemm_tile: null context");
     bool ok = tokens == 0;
     for (int b : kGemmBN) ok = ok || tokens == b;
-    if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 64 or 128", tokens);
+    if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 32, 64 or 128", tokens);
     ctx->tune_gemm_bn = tokens;
     return 0;
 }
@@ -673,17 +673,26 @@ int gemm_check(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, 
     return 0;
 }
 
+// Token tile of the fused GEMM (measured on MI355X, Q4_K, bf16 X, cold
+// weights): 16 up to 32 tokens (two 16-token tiles at 33.6 us against 40.2
+// us for one 64-token tile on 14336x4096); 33-128 tokens 32 while that grid
+// fits one workgroup per CU, else 64 (48 tokens: 35.9 against 42.4 us on
+// 14336x4096, 33.6 against 40.0 on 6144x4096; 128 tokens on 14336x4096,
+// 448 workgroups: 61.0 against 44.0); 128 beyond.
+int fused_bn(int m, int n, int num_cu) {
+    if (m <= 32) return 16;
+    if (m <= 128) return (long long)((n + 127) / 128) * ((m + 31) / 32) <= num_cu ? 32 : 64;
+    return 128;
+}
+
 // the fused MFMA dequant-GEMM (gguf_gemm.hip) on checked arguments
 int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
                int x_dtype, int y_dtype, const char* api) {
-    // token tile (measured on MI355X, 14336x4096 Q4_K): 16 up to 32 tokens
-    // (two 16-token tiles at 33.6 us against 40.2 us for one 64-token tile),
-    // 64 up to 128 (twice the workgroups of 128-token tiles), 128 beyond;
     // the 16-token tile stages 128 k at a time (32-row weight tiles in
     // 512-thread workgroups), so it needs k % 128 == 0
-    int bn = m <= 32 ? 16 : (m <= 128 ? 64 : 128);
+    int bn = fused_bn(m, n, ctx->num_cu);
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
-    if (bn == 16 && k % 128) bn = 64;
+    if (bn == 16 && k % 128) bn = 32;
     const int bm = bn == 16 ? 32 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];
@@ -842,21 +851,21 @@ int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, i
 
 // Built-in route of cima_hip_gguf_gemm_slab.  Measured on MI355X (Q4_K,
 // bf16 X, fp32 Y, cold weights; fused / slab + hipBLASLt in us):
-//   14336x4096  m=16 18/54   m=64 42/56   m=128 44/62   m=256 70/76  m=384 107/79
-//   4096x14336  m=16 42/54   m=48 128/62  m=128 129/93  m=256 205/90
-//   4096x4096   m=16 13/32   m=48 39/34   m=192 64/47   m=256 64/38
-//   1024x4096   m=16 13/19   m=48 38/19   m=256 64/25
-//   6144x4096   m=48 39/39   m=128 40/45  m=192 65/50
-// The split-k 16-token tiles win up to 32 tokens everywhere.  The 64- and
-// 128-token tiles give one workgroup per 128 weight rows and token tile, and
+//   14336x4096  m=16 18/54   m=64 36/56   m=128 47/65   m=256 73/76  m=384 110/82
+//   4096x14336  m=16 43/54   m=48 106/61  m=128 106/91  m=256 206/91
+//   4096x4096   m=16 15/33   m=48 33/34   m=128 33/42   m=192 64/47  m=256 64/39
+//   1024x4096   m=16 13/19   m=48 32/19   m=256 63/25
+//   6144x4096   m=48 34/40   m=128 34/44  m=192 65/50
+// The split-k 16-token tiles win up to 32 tokens everywhere.  The 32-, 64-
+// and 128-token tiles give one workgroup per 128 weight rows and token tile, and
 // a narrow grid of long rows leaves most CUs idle: the slab route wins
 // there, and past 256 tokens, where the per-tile weight decode dominates.
-bool slab_route_pays(int m, int n, int k) {
+bool slab_route_pays(int m, int n, int k, int num_cu) {
     if (m <= 32) return false;
     if (m > 256) return true;
-    const int bn = m <= 128 ? 64 : 128;
+    const int bn = fused_bn(m, n, num_cu);
     const long long wgs = (long long)((n + 127) / 128) * ((m + bn - 1) / bn);
-    return wgs * 4096 < (long long)(bn == 64 ? 48 : 160) * k;
+    return wgs * 4096 < (long long)(bn <= 64 ? 48 : 160) * k;
 }
 
 size_t ws_cap_of(size_t rest) { return rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax; }
@@ -875,7 +884,7 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void*
     // slab layout: W as f16 [n, k] | X as f16 [m, k] (unless X is f16) | workspace
     const size_t wbytes = align256((size_t)n * k * 2);
     const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
-    const bool lib = ctx->gemm_lib_min > 0 ? m >= ctx->gemm_lib_min : slab_route_pays(m, n, k);
+    const bool lib = ctx->gemm_lib_min > 0 ? m >= ctx->gemm_lib_min : slab_route_pays(m, n, k, ctx->num_cu);
     if (!lib || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
         return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
     // the library route is taken only if hipBLASLt has a plan for the shape:

@@ -14,7 +14,7 @@
 // accumulation.  LDS is double-buffered; the global loads of the next PF
 // stages are in flight in registers while a stage is multiplied.  Three
 // kernels: gemm_body_sk16 (16 tokens, four k-splits, weights dequantised
-// into the A operand registers, 16x16x32 MFMA), gemm_body_ra (64 tokens,
+// into the A operand registers, 16x16x32 MFMA), gemm_body_ra (32 or 64 tokens,
 // weights into the A operand registers, 32x32x16 MFMA) and
 // gemm_body_wide (128 tokens, weights through LDS, 32x32x16 MFMA).
 
@@ -283,6 +283,7 @@ struct XTile {
 // through LDS; at m = 256 / 512 the LDS-staged 2 x 2 grid is faster (68 /
 // 105 us against 72 / 112).
 template <int BN> struct GemmTile;
+template <> struct GemmTile<32> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
 
@@ -637,7 +638,7 @@ constexpr int ra_pf() {
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
-        else if constexpr (BN == 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
+        else if constexpr (BN <= 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
         else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
     }
 #define GEMM_XY(FN, D, BN)                                                    \
@@ -647,7 +648,7 @@ constexpr int ra_pf() {
     GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F16, f16)                          \
     GEMM_KERNEL(FN, D, BN, XT_F16, f16, XT_F16, f16)                          \
     GEMM_KERNEL(FN, D, BN, XT_BF16, bf16, XT_F16, f16)
-#define GEMM_FMT(FN, D) GEMM_XY(FN, D, 16) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
+#define GEMM_FMT(FN, D) GEMM_XY(FN, D, 16) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
 
 GEMM_FMT(q8_0, DQ8_0)
 GEMM_FMT(q4_0, DQ4_0)

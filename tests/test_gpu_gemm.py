@@ -83,7 +83,7 @@ def test_gemm_tile_variants_agree(hip):
     x = torch.from_numpy(xf).to(torch.float16).cuda()
     want = oracle.gemm(x.float().cpu().numpy(), w16, m, n, k)
     lib = hip.lib
-    for bn in (16, 64, 128):
+    for bn in (16, 32, 64, 128):
         hip.handle  # noqa: B018
         rc = lib.cima_hip_set_gemm_tile(hip.handle, bn)
         assert rc == 0
@@ -112,7 +112,7 @@ def test_gemm_argument_errors(hip):
 
 
 @pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
-@pytest.mark.parametrize("bn", [16, 64, 128])
+@pytest.mark.parametrize("bn", [16, 32, 64, 128])
 def test_gemm_dequantises_bit_exactly(hip, t, bn):
     """With X the identity, Y = dequant(W)^T: every f16 weight the kernel
     multiplies, read back exactly (an f16 times 1.0, summed with exact
