@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the GGUF dequant-GEMV hot path on one MI355X.
 
-Workload: the batch-1 decode GEMVs of one Llama-3-8B
+Workload (benchmark config 2): the batch-1 decode GEMVs of one Llama-3-8B
 decoder layer with Q4_K weights -- q|k|v as one 6144 x 4096 matrix (4096 +
 1024 + 1024 rows), o (4096 x 4096, residual epilogue), the fused gate+up
 SwiGLU (2 x 14336 x 4096) and down (4096 x 14336, residual epilogue),

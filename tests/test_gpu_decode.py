@@ -355,7 +355,7 @@ def test_decode_graph_replay_matches_eager(hip):
 
 
 def test_decode_step_config5_full_size(hip):
-    """BASELINE config 5 (Qwen2.5-0.5B shape, Q8_0, KV prefilled to 2048):
+    """Benchmark config 5 (Qwen2.5-0.5B shape, Q8_0, KV prefilled to 2048):
     one step against the oracle at full size."""
     cfg = DecoderConfig()
     m = synthetic_model(cfg, seed=5)

@@ -57,7 +57,7 @@ def test_gemm_small_shapes(hip, t, m):
 
 @pytest.mark.parametrize("m", [16, 128, 512])
 def test_gemm_config4_full_shape(hip, m):
-    """BASELINE config 4: Q4_K W 14336x4096 x X (m tokens, bf16), Y fp32;
+    """Benchmark config 4: Q4_K W 14336x4096 x X (m tokens, bf16), Y fp32;
     checked on a sample of 256 weight rows against the CPU path."""
     n, k = 14336, 4096
     w = synth.weights(Q4_K, 60, 0.02, n, k)

@@ -69,7 +69,7 @@ def test_slab_route_all_formats(route_all, t, m):
 
 @pytest.mark.parametrize("m", [512, 600])
 def test_slab_route_config4_shape(hip, m):
-    """BASELINE config 4 shape (Q4_K W 14336x4096, X bf16, Y fp32) at and
+    """Benchmark config 4 shape (Q4_K W 14336x4096, X bf16, Y fp32) at and
     past the route threshold: library route, checked on 256 sampled rows
     against the CPU path and in full against the fused kernel."""
     n, k = 14336, 4096

@@ -154,7 +154,7 @@ def test_gemv_selftest_shapes(hip, t, n, k):
     assert rel(yg, oracle.gemv(w16, x, n, k)) <= 1e-3
 
 
-BASELINE_SHAPES = [
+BENCH_SHAPES = [
     (Q8_0, 4864, 896),      # config 1
     (Q4_K, 14336, 4096),    # config 2: gate / up
     (Q4_K, 4096, 14336),    # down
@@ -172,7 +172,7 @@ BASELINE_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("t,n,k", BASELINE_SHAPES, ids=[f"{NAMES[t]}-{n}x{k}" for t, n, k in BASELINE_SHAPES])
+@pytest.mark.parametrize("t,n,k", BENCH_SHAPES, ids=[f"{NAMES[t]}-{n}x{k}" for t, n, k in BENCH_SHAPES])
 def test_gemv_baseline_shapes_vs_cpu_path(hip, t, n, k):
     """Seeded N(0,0.02) weights, x ~ N(0,1): rel err <= 1e-3 vs the reference
     CPU path (decode to f16, fp32 dot) at the benchmark's full sizes."""
