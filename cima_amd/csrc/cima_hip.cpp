@@ -479,6 +479,10 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                     char name[96];
                     snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xt, yt);
                     if (!rc) rc = add(MOD_GEMM, name);
+                    if (bn == 16) {
+                        snprintf(name, sizeof name, "cima_gemm_%s_b16n_%s_%s", F->name, xt, yt);
+                        if (!rc) rc = add(MOD_GEMM, name);
+                    }
                 }
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_dequant_") + F->name);
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_gather_") + F->name);
@@ -693,10 +697,17 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     int bn = fused_bn(m, n, ctx->num_cu);
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
     if (bn == 16 && k % 128) bn = 32;
-    const int bm = bn == 16 ? 32 : 128;  // weight rows per workgroup (GemmTile in gguf_gemm.hip)
+    // 16-token tiles: 32 rows per 512-thread workgroup, or 16 rows per
+    // 256-thread workgroup (_b16n_) where 32-row tiles would leave CUs idle
+    // (measured on MI355X, Q4_K, bf16 X, m = 16: 37.3 against 41.8 us on
+    // 4096x14336, 11.1 against 12.9 on 4096x4096, 9.3 against 11.1 on
+    // 1024x4096; 25 against 18 on 14336x4096, which fills the CUs)
+    const bool narrow = bn == 16 && (n + 31) / 32 < ctx->num_cu;
+    const int bm = narrow ? 16 : (bn == 16 ? 32 : 128);  // weight rows per workgroup
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];
-    snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", F->name, bn, xn[x_dtype], y_dtype == CIMA_DT_F32 ? "f32" : "f16");
+    snprintf(name, sizeof name, "cima_gemm_%s_b%d%s_%s_%s", F->name, bn, narrow ? "n" : "", xn[x_dtype],
+             y_dtype == CIMA_DT_F32 ? "f32" : "f16");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
     const void* xa = x;
@@ -704,7 +715,7 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     void* ya = y;
     int mm = m, nn = n, kk = k, ld = ldy;
     void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
-    const unsigned threads = bn == 16 ? 512 : 256;
+    const unsigned threads = bn == 16 && !narrow ? 512 : 256;
     hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, threads, 1,
                                          1, 0, ctx->stream, args, nullptr);
     return e == hipSuccess ? 0 : hip_fail(e, api);

@@ -648,7 +648,22 @@ constexpr int ra_pf() {
     GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F16, f16)                          \
     GEMM_KERNEL(FN, D, BN, XT_F16, f16, XT_F16, f16)                          \
     GEMM_KERNEL(FN, D, BN, XT_BF16, bf16, XT_F16, f16)
-#define GEMM_FMT(FN, D) GEMM_XY(FN, D, 16) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
+// 16-row split-k tiles (four waves) for weights too narrow to fill the CUs
+// with 32-row tiles: the _b16n_ kernels
+#define GEMM_KERNEL_NARROW(FN, D, XT, XN, YT, YN)                                                   \
+    extern "C" __global__ __launch_bounds__(256, 4) void cima_gemm_##FN##_b16n_##XN##_##YN(         \
+        const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
+        gemm_body_sk16<D, XT, YT, 1, 1>(x, w, y, m, n, k, ldy);                                     \
+    }
+#define GEMM_XY_NARROW(FN, D)                                                 \
+    GEMM_KERNEL_NARROW(FN, D, XT_F32, f32, XT_F32, f32)                       \
+    GEMM_KERNEL_NARROW(FN, D, XT_F16, f16, XT_F32, f32)                       \
+    GEMM_KERNEL_NARROW(FN, D, XT_BF16, bf16, XT_F32, f32)                     \
+    GEMM_KERNEL_NARROW(FN, D, XT_F32, f32, XT_F16, f16)                       \
+    GEMM_KERNEL_NARROW(FN, D, XT_F16, f16, XT_F16, f16)                       \
+    GEMM_KERNEL_NARROW(FN, D, XT_BF16, bf16, XT_F16, f16)
+#define GEMM_FMT(FN, D) \
+    GEMM_XY(FN, D, 16) GEMM_XY_NARROW(FN, D) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
 
 GEMM_FMT(q8_0, DQ8_0)
 GEMM_FMT(q4_0, DQ4_0)

@@ -62,6 +62,8 @@ def test_code_object_holds_every_kernel():
             for xt in ("f32", "f16", "bf16"):
                 for yt in ("f32", "f16"):
                     assert f"cima_gemm_{f}_b{bn}_{xt}_{yt}".encode() in blobs["gemm"]
+                    if bn == 16:
+                        assert f"cima_gemm_{f}_b16n_{xt}_{yt}".encode() in blobs["gemm"]
 
 
 def test_stream_read_kernel_present():
@@ -233,6 +235,6 @@ def test_gemm_kernels_do_not_spill():
     left in scratch memory -- register pressure, or an aggregate copy the
     compiler does not promote -- turns each stage into scratch traffic)."""
     notes = _kernel_notes(cbuild.HSACOS["gemm"])
-    assert len(notes) == 9 * 4 * 6
+    assert len(notes) == 9 * 5 * 6
     spills = {k: v for k, v in notes.items() if v[1] > 0}
     assert not spills, spills

@@ -135,3 +135,22 @@ def test_gemm_dequantises_bit_exactly(hip, t, bn):
         hip.set_gemm_tile(0)
     got = y.T  # [n, k]
     assert np.array_equal(got[ok], want[ok]), (int(ok.sum()), np.argwhere(got[ok] != want[ok])[:4])
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
+@pytest.mark.parametrize("n", [8192, 8191, 1000])
+def test_gemm_16_token_tiles_wide_and_narrow(hip, t, n):
+    """Up to 32 tokens the weight's row count picks the split-k tile: 32 rows
+    per workgroup from 8192 rows (256 workgroups fill the CUs), 16 rows
+    (the _b16n_ kernels) below; both against the CPU path, ragged row
+    counts included."""
+    k, m = 256, 13
+    w = synth.weights(t, 140 + t, 0.02, n, k)
+    xf = synth.normal(141, 1.0, m * k).reshape(m, k)
+    w16 = oracle.dequant(t, w, n * k)
+    for xd, yd in ((gguf.DT_BF16, gguf.DT_F32), (gguf.DT_F32, gguf.DT_F16)):
+        y, xh = run(hip, t, w, xf, m, n, k, xd, yd, ldy=n + 4)
+        want = oracle.gemm(xh, w16, m, n, k)
+        tol = 1e-5 if xd != gguf.DT_F32 and yd == gguf.DT_F32 else 1e-3
+        assert rel(y[:, :n], want) <= tol, (xd, yd)
+        assert np.all(y[:, n:] == 3.0)
