@@ -66,7 +66,7 @@ class Decoder(ctypes.Structure):
         + [(n, ctypes.c_void_p) for n in (
             "x", "qkv", "act", "logits", "part", "slot", "ids", "pos")])
 
-E_INVALID, E_FORMAT, E_NO_KERNEL, E_NOT_INIT = -1, -2, -3, -4
+E_INVALID, E_FORMAT, E_NO_KERNEL, E_NOT_INIT, E_LIBRARY = -1, -2, -3, -4, -5
 
 
 class EngineError(RuntimeError):

@@ -238,3 +238,13 @@ def test_gemm_kernels_do_not_spill():
     assert len(notes) == 9 * 5 * 6
     spills = {k: v for k, v in notes.items() if v[1] > 0}
     assert not spills, spills
+
+
+def test_error_codes_match_header():
+    """The Python error-code constants are the header's CIMA_E_* values."""
+    from cima_amd import hip as h
+
+    text = open(os.path.join(os.path.dirname(__file__), "..", "include", "cima_hip.h")).read()
+    codes = {name: int(v) for name, v in re.findall(r"#define CIMA_(E_[A-Z_]+)\s+(-?\d+)", text)}
+    assert codes == {n: getattr(h, n) for n in codes}
+    assert set(codes) == {"E_INVALID", "E_FORMAT", "E_NO_KERNEL", "E_NOT_INIT", "E_LIBRARY"}
