@@ -22,7 +22,14 @@ largest share of a step, timed with HIP events on its launch stream;
 (decode to f16, fp32 dot) on a bounded sample of the same step, single
 threaded like the reference's loops and again on all host cores.
 
-Usage: python bench.py [--gpus 1] [--steps 320] [--warmup 64]
+Every figure is the median of --repeats timed runs (graph replays): the
+headline over exactly --steps layer steps per replay, each per-shape leg
+cold (copies cycled) and hot (one buffer), the decode step over
+--decode-tokens tokens split across the repeats.  The device's sustained
+read bandwidth is re-measured (1 GiB transfers) and reported beside the
+8 TB/s datasheet figure.
+
+Usage: python bench.py [--gpus 1] [--steps 320] [--warmup 64] [--repeats 21]
 """
 import argparse
 import json
@@ -46,6 +53,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=320)
     ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--repeats", type=int, default=21, help="timed replays; the median is reported")
     ap.add_argument("--cpu-steps", type=int, default=4, help="layer steps in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
@@ -122,6 +130,17 @@ def main():
         torch.cuda.synchronize()
         return g
 
+    def replay_ms(g):
+        """One replay of g bracketed by synchronisations, timed with HIP
+        events on torch's stream (the replay's launch stream)."""
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b)
+
     if args.calib:
         src = torch.empty(64 << 20, dtype=torch.float32, device=dev).normal_()
         dst = torch.empty_like(src)
@@ -133,46 +152,37 @@ def main():
     for L in layers[:2]:
         layer(L)
     torch.cuda.synchronize()
-    g_all = capture(lambda: [layer(L) for L in layers])
-
-    def run_steps(nsteps):
-        reps = max(1, (nsteps + N_LAYERS - 1) // N_LAYERS)
-        for _ in range(reps):
-            g_all.replay()
-        return reps * N_LAYERS
-
-    run_steps(args.warmup)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    # exactly --steps layer steps per replay (step i runs layer copy i % 32),
+    # and a --warmup-step graph run once before timing
+    g_steps = capture(lambda: [layer(layers[i % N_LAYERS]) for i in range(args.steps)])
+    if args.warmup > 0:
+        g_warm = capture(lambda: [layer(layers[i % N_LAYERS]) for i in range(args.warmup)])
+        g_warm.replay()
+        torch.cuda.synchronize()
+        del g_warm
     t0 = time.perf_counter()
-    e0.record()
-    steps = run_steps(args.steps)
-    e1.record()
-    torch.cuda.synchronize()
+    rep_ms = [replay_ms(g_steps) for _ in range(args.repeats)]
     wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1)
+    steps = args.steps
+    ms = float(np.median(rep_ms))
     ms_per_step = ms / steps
     value = step_bytes * steps / (ms / 1e3) / 1e9
+    del g_steps
 
-    # ---- per-shape us/call, cold: graph of back-to-back calls over copies
-    def time_calls(launch, bufs, calls=64, reps=3):
+    # ---- per-shape us/call: a graph of back-to-back calls, replayed
+    # --repeats times, median per call.  Cold: the calls cycle over copies
+    # of the weight (more bytes than the 256 MB last-level cache); hot: every
+    # call reads one buffer.
+    def time_calls(launch, bufs, calls=64, reps=None):
         g = capture(lambda: [launch(bufs[i % len(bufs)]) for i in range(calls)])
         g.replay()
         torch.cuda.synchronize()
-        best = None
-        for _ in range(reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            g.replay()
-            b.record()
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) * 1e3 / calls
-            best = us if best is None else min(best, us)
-        return best
+        us = [replay_ms(g) * 1e3 / calls for _ in range(reps or args.repeats)]
+        return float(np.median(us))
 
     per_shape = {}
     read_us = {}
+    hot_us = {}
     gemm_flops = {}
     gemm_route = {}
     # the roofline kernel: fused gate+up SwiGLU, cold over the 32 layers
@@ -180,6 +190,8 @@ def main():
     pair_us = time_calls(lambda L: ctx.gguf_gemv_swiglu(Q4_K, h, L["gate"], L["up"], None, None, act, FFN, HID),
                          layers)
     per_shape["q4_k gate+up swiglu 2x14336x4096"] = (pair_us, pair_bytes)
+    hot_us["q4_k gate+up swiglu 2x14336x4096"] = time_calls(
+        lambda L: ctx.gguf_gemv_swiglu(Q4_K, h, L["gate"], L["up"], None, None, act, FFN, HID), layers[:1])
     # the plain streaming-read rate of the same byte count, measured the same
     # way (cold copies, graph replay): what any kernel can reach here
     rbytes = 2 * wbytes(Q4_K, FFN, HID)
@@ -189,6 +201,16 @@ def main():
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
     pair_read_us = time_calls(lambda b: ctx.stream_read(b, rbytes, sink), rbufs)
     del rbufs
+    # the device's sustained read bandwidth, re-measured: the same read kernel
+    # over 1 GiB transfers (two buffers, so nothing is served from cache)
+    pbytes = 1 << 30
+    pbufs = [torch.empty(pbytes, dtype=torch.uint8, device=dev) for _ in range(2)]
+    for b in pbufs:
+        b.fill_(1)
+    peak_us = time_calls(lambda b: ctx.stream_read(b, pbytes, sink), pbufs, calls=8)
+    peak_measured = pbytes / peak_us / 1e3
+    del pbufs
+    torch.cuda.empty_cache()
     if not args.no_shapes:
         def shape_leg(name, t, n, k, copies_mb=600):
             w = synth.weights(t, 200 + n % 97, 0.02, n, k)
@@ -199,6 +221,7 @@ def main():
             calls = max(16, min(64, 2 * ncopy))
             us = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs, calls=calls)
             per_shape[name] = (us, wbytes(t, n, k) + 4 * (n + k))
+            hot_us[name] = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs[:1], calls=calls)
             # the streaming-read time of the same weight bytes, same method
             rb = w.nbytes // 16 * 16
             read_us[name] = time_calls(lambda b: ctx.stream_read(b, rb, sink), bufs, calls=calls)
@@ -231,6 +254,8 @@ def main():
             us = time_calls(lambda b: ctx.nf4_gemv(xs, b, b[n * k // 2:].view(torch.float32), qm, ys, n, k, bs),
                             bufs, calls=calls)
             per_shape[name] = (us, nb + 2 * (n + k))
+            hot_us[name] = time_calls(lambda b: ctx.nf4_gemv(xs, b, b[n * k // 2:].view(torch.float32), qm, ys, n, k,
+                                                             bs), bufs[:1], calls=calls)
             read_us[name] = time_calls(lambda b: ctx.stream_read(b, nb // 16 * 16, sink), bufs, calls=calls)
         for nm, (n, k) in [("nf4 14336x4096 (gate/up)", (FFN, HID)), ("nf4 4096x14336 (down)", (HID, FFN)),
                            ("nf4 4096x4096 (q/o)", (HID, HID))]:
@@ -250,12 +275,17 @@ def main():
             us = time_calls(lambda b: ctx.gguf_gemm_slab(Q4_K, gx, b, gy, m, FFN, HID, gslab), gbufs, calls=24)
             b = wbytes(Q4_K, FFN, HID) + 2 * m * HID + 4 * m * FFN
             per_shape[f"q4_k gemm 14336x4096 m={m} (config 4)"] = (us, b)
+            hot_us[f"q4_k gemm 14336x4096 m={m} (config 4)"] = time_calls(
+                lambda b: ctx.gguf_gemm_slab(Q4_K, gx, b, gy, m, FFN, HID, gslab), gbufs[:1], calls=24)
             gemm_flops[f"q4_k gemm 14336x4096 m={m} (config 4)"] = 2.0 * FFN * HID * m
 
     shapes_out = {}
     for name, (us, b) in per_shape.items():
         shapes_out[name] = {"us_per_call": round(us, 3), "gb_s": round(b / us / 1e3, 1),
-                            "hbm_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4), "bytes": b}
+                            "hbm_frac": round(b / us / 1e3 / PEAK_HBM_GBS, 4),
+                            "frac_of_measured_peak": round(b / us / 1e3 / peak_measured, 4), "bytes": b}
+        if name in hot_us:
+            shapes_out[name]["hot_us_per_call"] = round(hot_us[name], 3)
         if name in read_us:
             shapes_out[name]["read_ceiling_us"] = round(read_us[name], 3)
             shapes_out[name]["frac_of_read_ceiling"] = round(read_us[name] / us, 4)
@@ -276,8 +306,12 @@ def main():
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
                 "kernel": "cima_gemv_q4_k_r1_i1_f32_pair", "alg_bytes_per_launch": pair_bytes,
                 "avg_launch_us": round(pair_us, 3),
+                "hot_us": round(hot_us["q4_k gate+up swiglu 2x14336x4096"], 3),
                 "read_ceiling_gb_s": round(rbytes / pair_read_us / 1e3, 1),
-                "frac_of_read_ceiling": round(achieved / (rbytes / pair_read_us / 1e3), 4)}
+                "frac_of_read_ceiling": round(achieved / (rbytes / pair_read_us / 1e3), 4),
+                "peak_measured_gb_s": round(peak_measured, 1),
+                "frac_of_measured_peak": round(achieved / peak_measured, 4),
+                "peak_measured_how": "cima_stream_read over 1 GiB, two buffers cycled, graph replay, median"}
 
     # ---- config 5: whole greedy decode step of a Qwen2.5-0.5B-shaped Q8_0
     # model, KV prefilled to 2048, one graph replay per token
@@ -314,14 +348,19 @@ def main():
             dd.replay()
         torch.cuda.synchronize()
         p0 = dd.position()
-        dms = time_tokens(dd.replay, dd.stream, args.decode_tokens)
-        assert dd.position() == p0 + args.decode_tokens
+        # --repeats timed runs of decode_tokens / repeats tokens each; median
+        per_rep = max(1, args.decode_tokens // args.repeats)
+        tok_ms = [time_tokens(dd.replay, dd.stream, per_rep) for _ in range(args.repeats)]
+        dms = float(np.median(tok_ms))
+        assert dd.position() == p0 + per_rep * args.repeats
         kv_bytes = dcfg.n_layers * 2 * dcfg.kv_heads * dcfg.head_dim * 2 * (p0 + args.decode_tokens // 2)
         decode = {"workload": "qwen2.5-0.5b-shaped Q8_0 greedy decode step (24 layers, tied 151936 head), "
                               "KV prefilled to 2048, one hipGraph replay per token (5 launches/layer + 3)",
-                  "tok_s": round(1e3 / dms, 1), "ms_per_token": round(dms, 4), "tokens": args.decode_tokens,
+                  "tok_s": round(1e3 / dms, 1), "ms_per_token": round(dms, 4), "tokens": per_rep * args.repeats,
+                  "ms_per_token_min_max": [round(min(tok_ms), 4), round(max(tok_ms), 4)],
+                  "repeats": args.repeats, "tokens_per_repeat": per_rep,
                   "tok_s_without_graph": round(1e3 / eager_ms, 1),
-                  "context": [p0, p0 + args.decode_tokens],
+                  "context": [p0, p0 + per_rep * args.repeats],
                   "bytes_per_token": wbytes_tok + kv_bytes,
                   "gb_s": round((wbytes_tok + kv_bytes) / dms / 1e6, 1)}
         del dd
@@ -350,11 +389,29 @@ def main():
                 n, k = shapes[name]
                 oracle.gguf_gemv_packed(Q4_K, host[name], xin, n, k, threads=ncores)
         mt_s = time.perf_counter() - t0
+        # dequant only (the reference's dequant_host, src/quant.rs:578-597):
+        # one 14336 x 4096 Q4_K matrix decoded to f16, single thread
+        dq_us = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            oracle.dequant(Q4_K, host["gate"], FFN * HID)
+            dq_us.append((time.perf_counter() - t0) * 1e6)
+        cpu_model = "unknown"
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
         cpu = {"value": round(step_bytes * args.cpu_steps / cpu_s / 1e9, 4), "unit": "GB/s", "cores": 1,
                "kind": "port",
                "sample": f"{args.cpu_steps} layer steps (same 7 Q4_K GEMVs, same weights), single thread, "
                          f"{cpu_s:.1f} s; oracle/gguf_oracle.c decode-to-f16 + fp32 dot",
                "ms_per_step": round(cpu_s * 1e3 / args.cpu_steps, 1),
+               "cpu_model": cpu_model, "nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+               "dequant_only": {"us_per_call": round(float(np.median(dq_us)), 1), "cores": 1,
+                                "sample": "oracle dequant of one Q4_K 14336x4096 matrix to f16, median of 5"},
                "all_cores": {"value": round(step_bytes * args.cpu_steps / mt_s / 1e9, 4), "unit": "GB/s",
                              "cores": ncores, "ms_per_step": round(mt_s * 1e3 / args.cpu_steps, 1),
                              "sample": f"the same {args.cpu_steps} layer steps, rows over {ncores} threads, "
@@ -378,7 +435,9 @@ def main():
                                "cycled (cold HBM), hipGraph replay",
                    "bytes_per_step": step_bytes, "layers_cycled": N_LAYERS,
                    "hbm_frac_of_8TBs": round(value / PEAK_HBM_GBS, 4),
-                   "wall_s": round(wall, 3)},
+                   "wall_s": round(wall, 3), "repeats": args.repeats,
+                   "ms_per_step_min_max": [round(min(rep_ms) / steps, 5), round(max(rep_ms) / steps, 5)],
+                   "timing": "median of --repeats graph replays of exactly --steps layer steps"},
         "shapes": shapes_out,
         "decode_step": decode,
         "roofline": roofline,

@@ -13,6 +13,7 @@ Produces, in ``cima_amd/lib/``:
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import subprocess
 import sys
@@ -62,6 +63,25 @@ def _cmds():
     }
 
 
+STAMP = os.path.join(LIB, "build.stamp")
+
+
+def source_hash() -> str:
+    """Hash of everything the native artefacts are built from: the sources
+    and headers under csrc/ and include/, and the compile commands."""
+    h = hashlib.sha256()
+    for d in (CSRC, INCLUDE):
+        for name in sorted(os.listdir(d)):
+            path = os.path.join(d, name)
+            if os.path.isfile(path):
+                h.update(name.encode())
+                with open(path, "rb") as f:
+                    h.update(f.read())
+    for cmd in _cmds().values():
+        h.update(" ".join(cmd).encode())
+    return h.hexdigest()
+
+
 def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
@@ -74,8 +94,12 @@ def build(verbose: bool = False) -> None:
     """Compile every native artefact (always recompiles)."""
     os.makedirs(LIB, exist_ok=True)
     cmds = _cmds()
+    if os.path.exists(STAMP):
+        os.remove(STAMP)
     with ThreadPoolExecutor(max_workers=len(cmds)) as ex:
         outs = list(ex.map(_run, cmds.values()))
+    with open(STAMP, "w") as f:
+        f.write(source_hash() + "\n")
     if verbose:
         for o in outs:
             if o.strip():
@@ -83,7 +107,12 @@ def build(verbose: bool = False) -> None:
 
 
 def built() -> bool:
-    return all(os.path.exists(p) for p in (*HSACOS.values(), LIBHIP, LIBSYNTH))
+    """True when every artefact exists and was built from the sources as
+    they are now (the stamp written by build() matches source_hash())."""
+    if not all(os.path.exists(p) for p in (*HSACOS.values(), LIBHIP, LIBSYNTH, STAMP)):
+        return False
+    with open(STAMP) as f:
+        return f.read().strip() == source_hash()
 
 
 if __name__ == "__main__":

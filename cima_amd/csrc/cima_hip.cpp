@@ -273,14 +273,15 @@ struct GemvExt {
 // extra x source / epilogue of a decode-step GEMV
 enum GemvKind { GK_PLAIN = 0, GK_ATT = 1, GK_AMAX = 2 };
 
-// threads per GEMV workgroup (GNT in gguf_gemv.hip)
+// threads per GEMV workgroup when a kernel does not state it (GNT in
+// gguf_gemv.hip; the launch uses each kernel's own __launch_bounds__)
 const int kGemvThreads = 256;
 
 struct GemvPlan {
     int rows;        // R: rows per lane group
     int iters;       // unit steps per row and lane
     int lpr_shift;   // log2 of lanes per group (16..64, inside one wave)
-    unsigned grid;   // workgroups of kGemvThreads threads
+    unsigned grid;   // workgroups (of `threads` threads)
     unsigned lds;    // dynamic LDS bytes: x as two int8 planes + padding, scales, sums
     bool ring;       // item-ring main loop (_ring kernels)
     bool ringl;      // stepped item ring for long rows (_ringl kernels, launched with one unit per step)
@@ -314,9 +315,7 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     while (it < iters) it <<= 1;
     int rows = 1;  // measured fastest for every decode shape; 2 is kept for tuning
     if (ctx->tune_rows && have_shape(ctx->tune_rows, it)) rows = ctx->tune_rows;
-    long groups_per_wg = (long)(kGemvThreads / 64) * (64 / lpr);
     long row_groups = ((long)n + rows - 1) / rows;
-    long wgs = (row_groups + groups_per_wg - 1) / groups_per_wg;
     // the item-ring loop for large matrices of one- or two-unit rows (measured
     // faster from about 8 MB of weights up; smaller ones are latency-bound
     // and finish sooner with the plain double buffer)
@@ -330,7 +329,7 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     const bool ringl = !pair && rows == 1 && big && ctx->tune_ringl != 2 &&
                        (it == 8 || (ctx->tune_ringl == 1 && it >= 2));
     const bool ring = !pair && rows == 1 && it <= 2 && big && !ringl;
-    return GemvPlan{rows, it, log2i(lpr), (unsigned)wgs, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
+    return GemvPlan{rows, it, log2i(lpr), (unsigned)row_groups, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
 }
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
@@ -384,8 +383,15 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
              epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
+    int threads = kGemvThreads;
+    if (hipFuncGetAttribute(&threads, HIP_FUNC_ATTRIBUTE_MAX_THREADS_PER_BLOCK, f) != hipSuccess || threads < 64)
+        threads = kGemvThreads;
+    {
+        const long groups_per_wg = (long)(threads / 64) * (64 >> p.lpr_shift);
+        p.grid = (unsigned)(((long)p.grid + groups_per_wg - 1) / groups_per_wg);  // row groups -> workgroups
+    }
     int resident = 0;
-    hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, kGemvThreads, p.lds);
+    hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, threads, p.lds);
     if (oe != hipSuccess) return hip_fail(oe, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (resident < 1) resident = 1;
     // persistent grid: one workgroup per CU for the item ring and for Q8_0,
@@ -405,7 +411,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     ext.eps = eps;
     int nn = n, kk = k, mm = mode, ls = p.lpr_shift;
     void* args[] = {&xa, &w0, &w1, &b0, &b1, &yy, &nn, &kk, &mm, &ls, &ext};
-    return launch(ctx, f, p.grid, kGemvThreads, args, api, p.lds);
+    return launch(ctx, f, p.grid, (unsigned)threads, args, api, p.lds);
 }
 
 }  // namespace

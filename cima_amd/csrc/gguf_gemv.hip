@@ -325,7 +325,10 @@ struct IQ6_K {
 
 // Workgroup shape: one persistent workgroup of GNW waves per CU (a single
 // dispatch wave of workgroups across the chip; x is staged once per CU).
-constexpr int GNW = 4;
+#ifndef CIMA_GEMV_WAVES
+#define CIMA_GEMV_WAVES 4
+#endif
+constexpr int GNW = CIMA_GEMV_WAVES;
 constexpr int GNT = 64 * GNW;
 
 // Item-ring depth: row groups in flight per lane for items of one unit of
@@ -387,10 +390,6 @@ DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
 // set, the GEMV multiplies W by h = f16(sat(x) * rsqrt(mean(sat(x)^2) + eps)
 // * norm_w) instead of x -- h is rounded to f16 (f32 activations: kept in
 // fp32) as the reference's separate rmsnorm launch writes it (stage_x).
-#ifdef CIMA_PROBE_TIMES
-// per-workgroup timestamps of an instrumented build (never in the product)
-__device__ unsigned long long g_probe_ts[8192 * 16];
-#endif
 
 // x staging.  Thread t owns 16-element chunks t + GNT j (j < XB); their raw
 // loads are issued together before the GEMV's first weight rows, so x and
@@ -533,15 +532,6 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
         }
         inv = 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
     }
-#ifdef CIMA_PROBE_TIMES
-    {
-        uint32_t z = 0;
-#pragma unroll
-        for (int j = 0; j < XB; j++) z ^= xb.u[j][0].x ^ xb.u[j][XBatch<ACT, XB>::U - 1].w;
-        if (z == 0x9E3779B9u) xs[0] = 0.f;
-        if ((threadIdx.x & 63) == 0) g_probe_ts[blockIdx.x * 16 + 10 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime();
-    }
-#endif
 #pragma unroll
     for (int j = 0; j < XB; j++) {
         const int c = t + GNT * j;
@@ -559,9 +549,6 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
         }
         quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
     }
-#ifdef CIMA_PROBE_TIMES
-    if ((threadIdx.x & 63) == 0) g_probe_ts[blockIdx.x * 16 + 6 + (threadIdx.x >> 6)] = __builtin_amdgcn_s_memrealtime();
-#endif
     __syncthreads();
 }
 
@@ -674,9 +661,6 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
                           int mode, int lpr_shift, const GemvExt& ext) {
     extern __shared__ __align__(16) uint8_t lds[];
-#ifdef CIMA_PROBE_TIMES
-    if (threadIdx.x == 0) g_probe_ts[blockIdx.x * 16] = __builtin_amdgcn_s_memrealtime();
-#endif
     constexpr int S = PAIR ? 2 * R : R;  // weight row streams per lane
     uint8_t* xq = lds;
     float* xs = reinterpret_cast<float*>(lds + 2 * k + 16 * (k >> F::PADSH));
@@ -733,9 +717,6 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         } else {
             stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
         }
-#ifdef CIMA_PROBE_TIMES
-        if (threadIdx.x == 0) g_probe_ts[blockIdx.x * 16 + 1] = __builtin_amdgcn_s_memrealtime();
-#endif
     };
     unsigned long long best = 0ull;
     typename F::Xf xreg;
@@ -788,15 +769,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         }
     };
     auto wdot = [&](const typename F::Raw& w, const typename F::Xf& xf, int u) -> float {
-#ifdef CIMA_PROBE_NODOT
-        uint32_t wsum = 0;
-        const uint32_t* wp = reinterpret_cast<const uint32_t*>(&w);
-#pragma unroll
-        for (int e = 0; e < (int)(sizeof(typename F::Raw) / 4); e++) wsum = wsum * 0x9E3779B1u + wp[e];
-        return (float)wsum;
-#else
         return F::dot(w, xf, u);
-#endif
     };
 
     if constexpr (RING == 1) {
@@ -972,9 +945,6 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             compute(bufB, i + 1);
         }
     }
-#ifdef CIMA_PROBE_TIMES
-    if (lane == 0) g_probe_ts[blockIdx.x * 16 + 2 + wave] = __builtin_amdgcn_s_memrealtime();
-#endif
     if constexpr (AMAX) {
         __shared__ unsigned long long red[GNW];
 #pragma unroll

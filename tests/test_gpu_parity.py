@@ -426,3 +426,69 @@ def test_item_ring_matches_double_buffer(t):
             assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (n, k, dt)
     for c in ctxs.values():
         c.close()
+
+
+def swiglu64(g, u):
+    g = np.asarray(g, np.float64)
+    return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q8_0], ids=["q4_k", "q8_0"])
+@pytest.mark.parametrize("act", ["f32", "f16"])
+@pytest.mark.parametrize("with_bias", [False, True], ids=["nobias", "bias"])
+def test_swiglu_full_config2_shape(hip, t, act, with_bias):
+    """The benchmark's roofline kernel on its own launch plan: fused gate+up
+    SwiGLU at 2 x 14336 x 4096 (64 lanes per row), against the reference CPU
+    path (each row decoded to f16, fp32 dot) on the stacked [2n, k] weight,
+    then g / (1 + e^-g) * u in float64 (k_gemv_f16 mode 2, src/kernels.cu:
+    516-537).  Both the separate-weight entry point and mode 2 of the plain
+    GEMV on the stacked weight; rel <= 1e-3."""
+    n, k = 14336, 4096
+    w = synth.weights(t, seed=77 + t, stddev=0.02, rows=2 * n, k=k)
+    x = synth.normal(78, 1.0, k)
+    bias = synth.normal(79, 0.1, 2 * n) if with_bias else None
+    if act == "f16":
+        x = x.astype(np.float16).astype(np.float32)
+        if bias is not None:
+            bias = bias.astype(np.float16).astype(np.float32)
+    dots = oracle.gguf_gemv_packed(t, w, x, 2 * n, k, threads=16).astype(np.float64)
+    if bias is not None:
+        dots = dots + bias
+    want = swiglu64(dots[:n], dots[n:])
+    cast = (lambda a: dev(a.astype(np.float16))) if act == "f16" else dev
+    xd = cast(x)
+    ydt = torch.float16 if act == "f16" else torch.float32
+    wg, wu = dev(w[:n]), dev(w[n:])
+    bg = cast(bias[:n]) if bias is not None else None
+    bu = cast(bias[n:]) if bias is not None else None
+    y = torch.empty(n, dtype=ydt, device="cuda")
+    hip.gguf_gemv_swiglu(t, xd, wg, wu, bg, bu, y, n, k)
+    r = rel(host(y).astype(np.float64), want)
+    print(f"{NAMES[t]} swiglu 2x{n}x{k} {act} bias={with_bias}: rel {r:.2e}")
+    assert r <= 1e-3
+    y2 = torch.empty(n, dtype=ydt, device="cuda")
+    hip.gguf_gemv(t, xd, dev(w), cast(bias) if bias is not None else None, y2, n, k, 2)
+    assert rel(host(y2).astype(np.float64), want) <= 1e-3
+    # the two entry points run the same kernel on the same operands
+    assert np.array_equal(host(y2), host(y))
+
+
+@pytest.mark.parametrize("t", FORMATS, ids=fid)
+def test_swiglu_every_launch_plan(hip, t):
+    """Mode 2 (gate|up pair) under each (rows, lanes) plan the tuner can
+    pick, ragged n, against the CPU path + the SwiGLU closed form."""
+    n, k = 333, 1536
+    w = synth.weights(t, seed=23 + t, stddev=0.02, rows=2 * n, k=k)
+    x = synth.normal(24, 1.0, k)
+    dots = oracle.gguf_gemv_packed(t, w, x, 2 * n, k, threads=16)
+    want = swiglu64(dots[:n], dots[n:])
+    wd, xd = dev(w), dev(x)
+    try:
+        for rows in (1, 2):
+            for lpr in (16, 32, 64):
+                hip.set_gemv_tuning(rows, lpr)
+                y = torch.empty(n, dtype=torch.float32, device="cuda")
+                hip.gguf_gemv(t, xd, wd, None, y, n, k, 2)
+                assert rel(host(y), want) <= 1e-3, (rows, lpr)
+    finally:
+        hip.set_gemv_tuning(0, 0)
