@@ -153,8 +153,10 @@ const char* const kModuleFiles[NUM_MODULES] = {"cima_gemv_a.hsaco", "cima_gemv_b
 // decode-step kernels (cima_decode.hsaco)
 const char* const kDecodeKernels[] = {
     "cima_rmsnorm_f16",     "cima_rope_f16",        "cima_kv_append_f16",    "cima_attn_split_d64",
-    "cima_attn_reduce_d64", "cima_attn_decode_d64", "cima_attn_split_d128",  "cima_attn_reduce_d128",
-    "cima_attn_decode_d128", "cima_argmax_f16",     "cima_argmax_to_ids",    "cima_pos_bump"};
+    "cima_attn_reduce_d64", "cima_attn_split_d128", "cima_attn_reduce_d128", "cima_attn_decode_d64_c64",
+    "cima_attn_decode_d64_c128", "cima_attn_decode_d64_c256", "cima_attn_decode_d128_c64",
+    "cima_attn_decode_d128_c128", "cima_attn_decode_d128_c256", "cima_argmax_f16", "cima_argmax_to_ids",
+    "cima_pos_bump"};
 
 std::string default_code_dir() {
     Dl_info info;
@@ -268,6 +270,7 @@ struct GemvExt {
     int max_seq;
     const int* pos_dev;
     unsigned long long* slot;
+    int att_window;
 };
 
 // extra x source / epilogue of a decode-step GEMV
@@ -1003,11 +1006,21 @@ int attn_dim_ok(int dim) { return dim == 64 || dim == 128; }
 // positions per attention chunk the kernels stage at most (ATT_MAX_CSZ)
 const int kAttMaxChunk = 256;
 
+// query heads per workgroup of cima_attn_decode_d<dim>_c<cp> (AT_GMAX in
+// decode_ops.hip; 4 cp threads, chunks of up to cp positions) and its LDS
+// bytes (sizeof AttnLds2<dim, cp>)
+const int kAttGroup = 8;
+unsigned attn_fused_lds(int dim, int cp) {
+    const int nw = cp / 16, tt = dim / 16, ns = nw >= tt ? nw / tt : 1;
+    return (unsigned)(16 * (dim + 8) * 2 + dim * 2 + dim * 4 + cp * 17 * 4 + kAttGroup * 2 * 4 +
+                      cp * (dim + 16) * 2 + ns * dim * 16 * 4);
+}
+
 int attn_fused(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, int q_heads, int kv_heads,
-               int dim, int max_seq, int csz, int n_chunks, float theta, float scale, const int* pos_dev,
+               int dim, int max_seq, int csz, int n_chunks, float theta, float scale, int window, const int* pos_dev,
                const char* api) {
     if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || !attn_dim_ok(dim) || max_seq <= 0 || csz <= 0 ||
-        csz > kAttMaxChunk || n_chunks <= 0 || (long long)n_chunks * csz < max_seq)
+        csz > kAttMaxChunk || n_chunks <= 0 || (long long)n_chunks * csz < max_seq || window < 0)
         return fail(CIMA_E_INVALID,
                     "%s: q_heads=%d kv_heads=%d dim=%d max_seq=%d csz=%d n_chunks=%d (dim 64 or 128, q_heads a "
                     "multiple of kv_heads, csz <= 256, n_chunks * csz >= max_seq)",
@@ -1015,11 +1028,16 @@ int attn_fused(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* pa
     if (!qkv || !kc || !vc || !part || !pos_dev) return fail(CIMA_E_INVALID, "%s: null pointer", api);
     if (!aligned(kc, 16) || !aligned(vc, 16) || !aligned(qkv, 4))
         return fail(CIMA_E_INVALID, "%s: misaligned cache (16 B) or qkv (4 B)", api);
+    // the narrowest workgroup whose chunk covers csz positions
+    const int cp = csz <= 64 ? 64 : (csz <= 128 ? 128 : 256);
     char name[48];
-    snprintf(name, sizeof name, "cima_attn_decode_d%d", dim);
+    snprintf(name, sizeof name, "cima_attn_decode_d%d_c%d", dim, cp);
     void* args[] = {&qkv, &kc, &vc, &part, &q_heads, &kv_heads, &max_seq, &csz, &n_chunks, &theta, &scale,
-                    &pos_dev};
-    return launch_named(ctx, name, (unsigned)(q_heads * n_chunks), 256, args, api);
+                    &window, &pos_dev};
+    const int grp = q_heads / kv_heads, hgs = (grp + kAttGroup - 1) / kAttGroup;
+    hipFunction_t f;
+    if (int rc = get_fn(ctx, name, &f)) return rc;
+    return launch(ctx, f, (unsigned)(kv_heads * hgs * n_chunks), 4 * cp, args, api, attn_fused_lds(dim, cp));
 }
 
 }  // namespace
@@ -1090,18 +1108,20 @@ int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_
 
 int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, int q_heads,
                          int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
-                         const int* pos_dev) {
+                         int window, const int* pos_dev) {
     const char* api = "cima_hip_attn_decode";
     if (int rc = ready(ctx, api)) return rc;
-    return attn_fused(ctx, qkv, kc, vc, part, q_heads, kv_heads, dim, max_seq, csz, n_chunks, theta, scale, pos_dev,
-                      api);
+    return attn_fused(ctx, qkv, kc, vc, part, q_heads, kv_heads, dim, max_seq, csz, n_chunks, theta, scale, window,
+                      pos_dev, api);
 }
 
 int cima_hip_attn_gguf_gemv(cima_hip_ctx* ctx, int t, const float* part, int q_heads, int dim, int csz, int n_chunks,
-                            int max_seq, const int* pos_dev, const void* w, const void* bias, void* y, int n, int mode) {
+                            int max_seq, int window, const int* pos_dev, const void* w, const void* bias, void* y,
+                            int n, int mode) {
     const char* api = "cima_hip_attn_gguf_gemv";
     if (int rc = ready(ctx, api)) return rc;
-    if (q_heads <= 0 || !attn_dim_ok(dim) || csz <= 0 || n_chunks <= 0 || max_seq <= 0 || (mode != 0 && mode != 1))
+    if (q_heads <= 0 || !attn_dim_ok(dim) || csz <= 0 || n_chunks <= 0 || max_seq <= 0 || window < 0 ||
+        (mode != 0 && mode != 1))
         return fail(CIMA_E_INVALID, "%s: q_heads=%d dim=%d csz=%d n_chunks=%d max_seq=%d mode=%d", api, q_heads, dim,
                     csz, n_chunks, max_seq, mode);
     if (!part || !pos_dev) return fail(CIMA_E_INVALID, "%s: null partials or position", api);
@@ -1112,6 +1132,7 @@ int cima_hip_attn_gguf_gemv(cima_hip_ctx* ctx, int t, const float* part, int q_h
     ext.att_dim = dim;
     ext.max_seq = max_seq;
     ext.pos_dev = pos_dev;
+    ext.att_window = window;
     return gemv_common(ctx, t, part, w, nullptr, bias, nullptr, y, n, q_heads * dim, mode, CIMA_DT_F16, false, api,
                        nullptr, 0.f, GK_ATT, &ext);
 }
@@ -1201,11 +1222,11 @@ int cima_hip_decode_step(cima_hip_ctx* ctx, const cima_decoder* d) {
         }
         // rope q, k; kv append; split attention (:1100-1160)
         if (int rc = attn_fused(ctx, d->qkv, L.k_cache, L.v_cache, d->part, d->q_heads, d->kv_heads, hd, d->max_seq,
-                                csz, nch, d->rope_theta, scale, d->pos, api))
+                                csz, nch, d->rope_theta, scale, L.window, d->pos, api))
             return rc;
         // merge of the partials -> o projection + residual (:1161-1238)
-        if (int rc = cima_hip_attn_gguf_gemv(ctx, ty(L.type_o), d->part, d->q_heads, hd, csz, nch, d->max_seq, d->pos,
-                                             L.wo, nullptr, d->x, d->hidden, 1))
+        if (int rc = cima_hip_attn_gguf_gemv(ctx, ty(L.type_o), d->part, d->q_heads, hd, csz, nch, d->max_seq,
+                                             L.window, d->pos, L.wo, nullptr, d->x, d->hidden, 1))
             return rc;
         // rmsnorm -> gate|up SwiGLU -> down + residual (:1240-1260)
         if (!L.w_up) {

@@ -15,16 +15,8 @@
 // |v| clamped to 65000 (g_sat16, src/kernels.cu:30-35)
 DEV float sat16(float v) { return fmaxf(fminf(v, 65000.f), -65000.f); }
 
-DEV float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
-}
-DEV float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
-}
+DEV float wave_sum(float v) { return wave_sum_u(v); }
+DEV float wave_max(float v) { return wave_max_u(v); }
 
 // ------------------------------------------------------------------ RMSNorm
 
@@ -301,63 +293,278 @@ DEV void attn_reduce_body(const float* __restrict__ part, uint16_t* __restrict__
 }
 
 // Decode attention partials of one layer at position pos = *pos_dev, with
-// RoPE and the KV append folded in:
+// RoPE and the KV append folded in (replaces k_rope x2 + k_kv_append +
+// k_attn_decode_split, src/models/transformer.rs:1100-1160):
 //   qkv = [q (q_heads*D) | k (kv_heads*D) | v (kv_heads*D)] f16, the output
-//   of the fused q/k/v GEMV (biases applied, RoPE not yet);
-//   every workgroup (query head h, chunk ci) rotates its q; the chunk that
-//   holds pos also rotates the new k, takes the new k and v from LDS for
-//   position pos, and (first head of each kv group) appends them to the
-//   cache.  The partials are merged by the consumer: attn_reduce, or the
-//   o-projection GEMV's x staging (cima_hip_attn_gguf_gemv).
-// Replaces k_rope x2 + k_kv_append + k_attn_decode_split
-// (src/models/transformer.rs:1100-1160).
-template <int D>
+//   of the fused q/k/v GEMV (biases applied, RoPE not yet).
+//
+// One workgroup of CP / 16 waves per (kv head, group of up to AT_GMAX of
+// its query heads, chunk of csz <= CP positions): the chunk's keys and
+// values are read once for every query head that shares them (GQA).
+// Everything the workgroup reads is addressed without the position -- the
+// chunk's cache rows, the group's q, the new k and v -- so those loads go
+// out together with the load of *pos_dev and the kernel pays one memory
+// round trip; rows past the live length are selected away (never
+// multiplied: they may hold anything).  The chunk holding pos takes the new
+// position's key and value from LDS and, in the first head group, appends
+// them to the cache.  window > 0 keeps the last `window` positions (the
+// split kernel's wlo, src/kernels.cu:557-559).
+//
+// Both contractions run on the matrix cores.  Scores: wave w takes
+// positions [16 w, 16 w + 16) and computes S^T = K Q^T with f16 MFMA
+// (16x16x16, fp32 accumulate; K and the f16-rounded rotated q are exact
+// f16 operands, so this is the fp32 dot of the reference up to summation
+// order); its key rows go straight from HBM into the A operand (lane l:
+// row l % 16, a contiguous D/4-dim slice, the k order permuted alike in A
+// and B).  Softmax: wave h < g, head h, over the chunk, with DPP
+// reductions.  Value sum: O^T = V^T P^T with fp32 MFMA (16x16x4): the
+// probabilities stay fp32, V^T is read from the LDS copy of the value rows;
+// waves split dims into 16-wide tiles and, where waves outnumber tiles,
+// positions into ranges whose partial sums add through LDS in a fixed
+// order.
+constexpr int AT_GMAX = 8;                      // query heads per workgroup
+
+typedef _Float16 at_half4 __attribute__((ext_vector_type(4)));
+typedef float at_float4 __attribute__((ext_vector_type(4)));
+
+template <int D, int CP>
+struct AttnLds2 {
+    static constexpr int NW = CP / 16;          // waves
+    static constexpr int TT = D / 16;           // 16-dim tiles of the value sum
+    static constexpr int NS = NW >= TT ? NW / TT : 1;  // position ranges of the value sum
+    static constexpr int VS = D + 16;           // f16 stride of a value row (padded: no bank conflicts)
+    static constexpr int QS = D + 8;            // f16 stride of a query row
+    static constexpr int PS = 17;               // fp32 stride of a probability row
+    uint16_t q[16][QS];                         // rotated queries, f16; rows >= g zero
+    uint16_t kn[D];                             // the new position's rotated key, f16
+    float vn[D];                                // the new position's value
+    float p[CP][PS];                            // per position: scores, then e^(s - m), per head
+    float ml[AT_GMAX][2];                       // per head: m, l
+    uint16_t v[CP][VS];                         // the chunk's value rows (dead rows zero)
+    float red[NS][D][16];                       // value-sum partials per position range
+};
+
+template <int D, int CP>
 DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
                          float* __restrict__ part, int q_heads, int kv_heads, int max_seq, int csz, int n_chunks,
-                         float theta, float scale, const int* __restrict__ pos_dev) {
-    __shared__ AttnLds<D> L;
-    const int t = threadIdx.x;
-    const int pos = *pos_dev;
-    const int seq = min(pos + 1, max_seq);
-    const int h = blockIdx.x / n_chunks, ci = blockIdx.x % n_chunks;
-    const int grp = q_heads / kv_heads, kvh = h / grp;
-    const int s0 = ci * csz, s1 = min(s0 + csz, seq);
-    if (s0 >= s1) return;
-    const bool has_new = pos < max_seq && s0 <= pos && pos < s1;
+                         float theta, float scale, int window, const int* __restrict__ pos_dev) {
+    extern __shared__ __align__(16) uint8_t at_lds[];
+    using Lds = AttnLds2<D, CP>;
+    Lds& L = *reinterpret_cast<Lds*>(at_lds);
+    constexpr int NW = Lds::NW, TT = Lds::TT, NS = Lds::NS;
+    constexpr int TPW = NW >= TT ? 1 : TT / NW;  // value-sum tiles per wave
+    constexpr int PR = CP / NS;                  // positions per value-sum range
+    constexpr int KD = D / 4;                    // key dims per lane (A operand)
+    constexpr int NK = KD / 8;                   // uint4 per lane
+    constexpr int NT = 4 * CP;                   // threads
+    static_assert(NW * 64 == NT && TT % (NW >= TT ? 1 : NW) == 0 && PR % 4 == 0, "attention tile shape");
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int lr = lane & 15, lg = lane >> 4;    // MFMA row / column (lr), lane group (lg)
+    const int grp = q_heads / kv_heads;
+    const int hgs = (grp + AT_GMAX - 1) / AT_GMAX;
+    const int ci = blockIdx.x % n_chunks;
+    const int hg = (blockIdx.x / n_chunks) % hgs;
+    const int kvh = blockIdx.x / n_chunks / hgs;
+    const int qh0 = kvh * grp + hg * AT_GMAX;
+    const int g = min(AT_GMAX, grp - hg * AT_GMAX);
+    const int s0 = ci * csz;
     uint16_t* kh = kc + (size_t)kvh * max_seq * D;
     uint16_t* vh = vc + (size_t)kvh * max_seq * D;
-    // the chunk's cache loads go out first; the new position's row (not yet
-    // in the cache) is taken from LDS
-    AttnRegs<D> R;
-    attn_issue<D>(R, kh, vh, s0, s1);
-    const float p = (float)pos;
-    if (t < D / 2) {
-        const uint16_t* qh = qkv + (size_t)h * D;
-        float oa, ob;
-        rope_rot(h2f(qh[t]), h2f(qh[t + D / 2]), p, t, D, theta, oa, ob);
-        L.q[t] = h2f(f2h(oa));
-        L.q[t + D / 2] = h2f(f2h(ob));
-    } else if (has_new && t < D) {
-        const int i = t - D / 2;
-        const uint16_t* kn = qkv + (size_t)q_heads * D + (size_t)kvh * D;
-        float oa, ob;
-        rope_rot(h2f(kn[i]), h2f(kn[i + D / 2]), p, i, D, theta, oa, ob);
-        const uint32_t ha = f2h(oa), hb = f2h(ob);
-        L.kn[i] = h2f(ha);
-        L.kn[i + D / 2] = h2f(hb);
-        if (h % grp == 0) {
-            kh[(size_t)pos * D + i] = (uint16_t)ha;
-            kh[(size_t)pos * D + i + D / 2] = (uint16_t)hb;
+
+    // ---- loads that do not depend on the position
+    // key rows in the A layout: lane l of wave w holds dims [KD lg, +KD) of
+    // position s0 + 16 w + lr
+    const int kp = 16 * wave + lr;
+    uint4 kr[NK];
+    {
+        const int row = min(s0 + min(kp, csz - 1), max_seq - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(kh + (size_t)row * D + KD * lg);
+#pragma unroll
+        for (int j = 0; j < NK; j++) kr[j] = src[j];
+    }
+    // value rows, contiguous: thread t holds 16 bytes (8 dims) of row
+    // t / (D / 8), for CP * D / 8 / NT row slices per thread
+    constexpr int VPT = CP * (D / 8) / NT;       // = D / 32
+    uint4 vr[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; j++) {
+        const int e = t + NT * j, r = e / (D / 8), c8 = e % (D / 8);
+        const int row = min(s0 + min(r, csz - 1), max_seq - 1);
+        vr[j] = reinterpret_cast<const uint4*>(vh + (size_t)row * D)[c8];
+    }
+    // rotation operands: item e < g*D/2 is pair e % (D/2) of query head
+    // e / (D/2); the next D/2 items the new key's pairs; the next D the new
+    // value (thread t takes items t, t + NT, ...)
+    const int nq = g * (D / 2);
+    constexpr int RI = (AT_GMAX * (D / 2) + D / 2 + D + NT - 1) / NT;  // items per thread
+    uint32_t ra[RI], rb[RI];
+#pragma unroll
+    for (int j = 0; j < RI; j++) {
+        const int e = t + NT * j;
+        ra[j] = rb[j] = 0;
+        if (e < nq) {
+            const uint16_t* qh = qkv + (size_t)(qh0 + e / (D / 2)) * D;
+            ra[j] = qh[e % (D / 2)];
+            rb[j] = qh[e % (D / 2) + D / 2];
+        } else if (e < nq + D / 2) {
+            const uint16_t* kn = qkv + (size_t)q_heads * D + (size_t)kvh * D;
+            ra[j] = kn[e - nq];
+            rb[j] = kn[e - nq + D / 2];
+        } else if (e < nq + D / 2 + D) {
+            ra[j] = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + (e - nq - D / 2)];
         }
-    } else if (has_new && t >= D && t < 2 * D) {
-        const int i = t - D;
-        const uint16_t vv = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + i];
-        L.vn[i] = h2f(vv);
-        if (h % grp == 0) vh[(size_t)pos * D + i] = vv;
+    }
+    const int pos = *pos_dev;
+    const int seq = min(pos + 1, max_seq);
+    const int wlo = (window > 0 && seq > window) ? seq - window : 0;
+    const int lo = max(s0, wlo), hi = min(s0 + csz, seq);
+    if (lo >= hi) return;
+    const bool has_new = pos < max_seq && s0 <= pos && pos < s0 + csz;
+    auto live = [&](int r) { return r < csz && s0 + r >= lo && s0 + r < hi; };
+
+    // ---- RoPE of the group's queries and the new key; the append; rows
+    // g..15 of the query block are zero
+    const float fp = (float)pos;
+#pragma unroll
+    for (int j = 0; j < RI; j++) {
+        const int e = t + NT * j;
+        if (e < nq) {
+            const int h = e / (D / 2), i = e % (D / 2);
+            float oa, ob;
+            rope_rot(h2f(ra[j]), h2f(rb[j]), fp, i, D, theta, oa, ob);
+            L.q[h][i] = (uint16_t)f2h(oa);
+            L.q[h][i + D / 2] = (uint16_t)f2h(ob);
+        } else if (has_new && e < nq + D / 2) {
+            const int i = e - nq;
+            float oa, ob;
+            rope_rot(h2f(ra[j]), h2f(rb[j]), fp, i, D, theta, oa, ob);
+            const uint32_t ha = f2h(oa), hb = f2h(ob);
+            L.kn[i] = (uint16_t)ha;
+            L.kn[i + D / 2] = (uint16_t)hb;
+            if (hg == 0) {
+                kh[(size_t)pos * D + i] = (uint16_t)ha;
+                kh[(size_t)pos * D + i + D / 2] = (uint16_t)hb;
+            }
+        } else if (has_new && e < nq + D / 2 + D) {
+            const int i = e - nq - D / 2;
+            L.vn[i] = h2f(ra[j]);
+            if (hg == 0) vh[(size_t)pos * D + i] = (uint16_t)ra[j];
+        }
+    }
+    for (int e = t; e < (16 - g) * D; e += NT) L.q[g + e / D][e % D] = 0;
+    __syncthreads();
+
+    // ---- value rows -> LDS (dead rows as zeros; the new position from vn)
+#pragma unroll
+    for (int j = 0; j < VPT; j++) {
+        const int e = t + NT * j, r = e / (D / 8), c8 = e % (D / 8);
+        uint4 w = vr[j];
+        if (has_new && s0 + r == pos) {
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) o[k] = f2h2(L.vn[8 * c8 + 2 * k], L.vn[8 * c8 + 2 * k + 1]);
+            w = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+        if (!live(r)) w = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4*>(&L.v[r][8 * c8]) = w;
+    }
+
+    // ---- scores S^T (positions x heads) of wave `wave`'s 16 positions
+    if (has_new && s0 + kp == pos) {
+#pragma unroll
+        for (int j = 0; j < NK; j++) kr[j] = reinterpret_cast<const uint4*>(&L.kn[KD * lg])[j];
+    }
+    at_float4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NK; j++) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(&L.q[lr][KD * lg + 8 * j]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(at_half4, make_uint2(kr[j].x, kr[j].y)),
+                                                     __builtin_bit_cast(at_half4, make_uint2(qv.x, qv.y)), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(at_half4, make_uint2(kr[j].z, kr[j].w)),
+                                                     __builtin_bit_cast(at_half4, make_uint2(qv.z, qv.w)), acc, 0, 0, 0);
+    }
+    // lane l holds S[position 16 wave + 4 lg + i][head lr]
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = 16 * wave + 4 * lg + i;
+        L.p[r][lr] = live(r) ? acc[i] * scale : -INFINITY;
     }
     __syncthreads();
-    attn_chunk<D>(L, R, s0, s1, has_new ? pos : -1, scale, part + ((size_t)h * n_chunks + ci) * (D + 2));
+
+    // ---- softmax of heads wave, wave + NW, ... over the chunk
+    for (int h = wave; h < g; h += NW) {
+        constexpr int SP = CP / 64;      // scores per lane
+        float sc[SP];
+        float m = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < SP; i++) {
+            sc[i] = L.p[lane + 64 * i][h];
+            m = fmaxf(m, sc[i]);
+        }
+        m = wave_max_u(m);
+        float l = 0.f;
+#pragma unroll
+        for (int i = 0; i < SP; i++) {
+            const float e = sc[i] == -INFINITY ? 0.f : __expf(sc[i] - m);
+            L.p[lane + 64 * i][h] = e;
+            l += e;
+        }
+        l = wave_sum_u(l);
+        if (lane == 0) {
+            L.ml[h][0] = m;
+            L.ml[h][1] = l;
+        }
+    }
+    __syncthreads();
+
+    // ---- value sum O^T (dims x heads): tile(s) of 16 dims over a range of
+    // PR positions, 4 positions per fp32 MFMA step
+    {
+        const int split = NW >= TT ? wave / TT : 0;
+        const int tile0 = NW >= TT ? wave % TT : wave * TPW;
+        at_float4 o[TPW];
+#pragma unroll
+        for (int u = 0; u < TPW; u++) o[u] = (at_float4){0.f, 0.f, 0.f, 0.f};
+        const int pb = split * PR;
+#pragma unroll 4
+        for (int st = 0; st < PR / 4; st++) {
+            const int r = pb + 4 * st + lg;
+            const float pv = L.p[r][lr];
+#pragma unroll
+            for (int u = 0; u < TPW; u++) {
+                const float vv = h2f(L.v[r][16 * (tile0 + u) + lr]);
+                o[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, pv, o[u], 0, 0, 0);
+            }
+        }
+        // lane l holds O[dim 16 tile + 4 lg + i][head lr]
+#pragma unroll
+        for (int u = 0; u < TPW; u++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) L.red[split][16 * (tile0 + u) + 4 * lg + i][lr] = o[u][i];
+    }
+    __syncthreads();
+    for (int e = t; e < g * D; e += NT) {
+        const int h = e / D, d = e % D;
+        float s = 0.f;
+#pragma unroll
+        for (int sp = 0; sp < NS; sp++) s += L.red[sp][d][h];
+        float* dst = part + ((size_t)(qh0 + h) * n_chunks + ci) * (D + 2);
+        dst[2 + d] = s;
+        if (d == 0) {
+            dst[0] = L.ml[h][0];
+            dst[1] = L.ml[h][1];
+        }
+    }
 }
+
+// cima_attn_decode_d<D>_c<CP>: 4 CP threads, chunks of up to CP positions
+#define ATTN_FUSED(D, CP)                                                                                        \
+    extern "C" __global__ __launch_bounds__(4 * CP) void cima_attn_decode_d##D##_c##CP(                          \
+        const uint16_t* qkv, uint16_t* kc, uint16_t* vc, float* part, int q_heads, int kv_heads, int max_seq,    \
+        int csz, int n_chunks, float theta, float scale, int window, const int* pos_dev) {                       \
+        attn_fused_body<D, CP>(qkv, kc, vc, part, q_heads, kv_heads, max_seq, csz, n_chunks, theta, scale,       \
+                               window, pos_dev);                                                                 \
+    }
 
 #define ATTN_KERNELS(D)                                                                                          \
     extern "C" __global__ __launch_bounds__(256) void cima_attn_split_d##D(                                      \
@@ -371,11 +578,7 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
         const int* pos_dev) {                                                                                    \
         attn_reduce_body<D>(part, out, csz, n_chunks, seq, max_seq, window, pos_dev);                            \
     }                                                                                                            \
-    extern "C" __global__ __launch_bounds__(256) void cima_attn_decode_d##D(                                     \
-        const uint16_t* qkv, uint16_t* kc, uint16_t* vc, float* part, int q_heads, int kv_heads, int max_seq,    \
-        int csz, int n_chunks, float theta, float scale, const int* pos_dev) {                                   \
-        attn_fused_body<D>(qkv, kc, vc, part, q_heads, kv_heads, max_seq, csz, n_chunks, theta, scale, pos_dev); \
-    }
+    ATTN_FUSED(D, 64) ATTN_FUSED(D, 128) ATTN_FUSED(D, 256)
 
 ATTN_KERNELS(64)
 ATTN_KERNELS(128)

@@ -343,8 +343,7 @@ constexpr int GNT = 64 * GNW;
 // sum over the workgroup (every thread calls it; all get the total)
 DEV float block_sum(float v) {
     __shared__ float red[GNW];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    v = wave_sum_u(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float t = 0.f;
@@ -563,6 +562,7 @@ struct GemvExt {
     int max_seq;               //   cache length,
     const int* pos_dev;        //   current position (live length *pos_dev + 1)
     unsigned long long* slot;  // argmax epilogue target
+    int att_window;            //   sliding window (> 0: the last att_window positions)
 };
 
 // Attention-merge x source: x[h*D + d] = f16(sum_c e^(m_c - M) acc_c[d] /
@@ -582,19 +582,44 @@ DEV void merge_step(float& M, float& L, float a[16], float m2, float l2, const f
     M = Mn;
 }
 
+// The first ATT_PRE partials of each lane (chunks sub, sub + 4, ...) are
+// loaded before the position is read -- their addresses do not depend on
+// it -- so the merge costs one memory round trip; chunks past the live
+// length or wholly before the window are skipped, never multiplied (they
+// may hold anything).
+constexpr int ATT_PRE = 3;
+
 DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, float* xt) {
     const int D = ext.att_dim, nch = ext.att_chunks, csz = ext.att_csz;
-    const int seq = min(*ext.pos_dev + 1, ext.max_seq);
-    const int active = min((seq + csz - 1) / csz, nch);
     for (int idx = threadIdx.x; idx < (k >> 2); idx += GNT) {
         const int e0 = (idx >> 2) * 16, sub = idx & 3;
         const int h = e0 / D, d0 = e0 - h * D;
         const float* ph = part + (size_t)h * nch * (D + 2);
+        float2 pml[ATT_PRE];
+        float pb[ATT_PRE][16];
+#pragma unroll
+        for (int j = 0; j < ATT_PRE; j++) {
+            const float* pc = ph + (size_t)min(sub + 4 * j, nch - 1) * (D + 2);
+            pml[j] = *reinterpret_cast<const float2*>(pc);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float2 v = reinterpret_cast<const float2*>(pc + 2 + d0)[i];
+                pb[j][2 * i] = v.x;
+                pb[j][2 * i + 1] = v.y;
+            }
+        }
+        const int seq = min(*ext.pos_dev + 1, ext.max_seq);
+        const int wlo = (ext.att_window > 0 && seq > ext.att_window) ? seq - ext.att_window : 0;
+        const int active = min((seq + csz - 1) / csz, nch), c0 = wlo / csz;
         float M = -INFINITY, L = 0.f, a[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) a[i] = 0.f;
-#pragma unroll 2
-        for (int c = sub; c < active; c += 4) {
+#pragma unroll
+        for (int j = 0; j < ATT_PRE; j++) {
+            const int c = sub + 4 * j;
+            if (c >= c0 && c < active) merge_step(M, L, a, pml[j].x, pml[j].y, pb[j]);
+        }
+        for (int c = max(sub + 4 * ATT_PRE, c0 + ((sub - c0) & 3)); c < active; c += 4) {
             const float* pc = ph + (size_t)c * (D + 2);
             const float2 ml = *reinterpret_cast<const float2*>(pc);
             float b[16];
@@ -606,13 +631,14 @@ DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, f
             }
             merge_step(M, L, a, ml.x, ml.y, b);
         }
-#pragma unroll
-        for (int o = 1; o <= 2; o <<= 1) {
-            const float m2 = __shfl_xor(M, o), l2 = __shfl_xor(L, o);
+        {  // the four lanes of a chunk combine: lane ^ 1, then lane ^ 2 (DPP)
             float b[16];
 #pragma unroll
-            for (int i = 0; i < 16; i++) b[i] = __shfl_xor(a[i], o);
-            merge_step(M, L, a, m2, l2, b);
+            for (int i = 0; i < 16; i++) b[i] = dpp_xor1(a[i]);
+            merge_step(M, L, a, dpp_xor1(M), dpp_xor1(L), b);
+#pragma unroll
+            for (int i = 0; i < 16; i++) b[i] = dpp_xor2(a[i]);
+            merge_step(M, L, a, dpp_xor2(M), dpp_xor2(L), b);
         }
         if (sub == 0) {
 #pragma unroll

@@ -43,6 +43,7 @@ class DecoderConfig:
     ggml_type: int = gguf.DType.Q8_0
     max_seq: int = 4096
     attn_chunk: int = 256
+    window: int = 0      # sliding-window attention (> 0: the last `window` positions), every layer
 
 
 # the projections of a layer, as named in a layer's "types" dict
@@ -107,6 +108,8 @@ def synthetic_model(cfg: DecoderConfig, seed: int = 5, sigma: float = 0.02,
             "w_down": synth.weights(types["down"], b + 7, sigma, cfg.hidden, cfg.ffn),
             "types": dict(types),
         }
+        if cfg.window:
+            L["window"] = int(cfg.window)
         if types["q"] == types["k"] == types["v"]:
             L["wqkv"] = synth.weights(types["q"], b + 2, sigma, qd + 2 * kvd, cfg.hidden)
         else:
@@ -150,8 +153,9 @@ class DeviceDecoder:
         self.final_norm = up(model.final_norm)
         self.layers = []
         for L in model.layers:
-            d = {k: (None if v is None else up(v)) for k, v in L.items() if k != "types"}
+            d = {k: (None if v is None else up(v)) for k, v in L.items() if k not in ("types", "window")}
             d["types"] = dict(L.get("types") or {})
+            d["window"] = int(L.get("window", c.window))
             d["k_cache"] = torch.zeros((c.kv_heads, c.max_seq, c.head_dim), dtype=torch.float16, device=dev)
             d["v_cache"] = torch.zeros_like(d["k_cache"])
             self.layers.append(d)
@@ -177,7 +181,7 @@ class DeviceDecoder:
             arr[i] = DecoderLayer(p(L["attn_norm"]), p(L["wqkv"]), p(L.get("bqkv")), p(L["wo"]), p(L["ffn_norm"]),
                                   p(L["w_gate_up"]), p(L["w_down"]), p(L["k_cache"]), p(L["v_cache"]),
                                   p(L.get("wk")), p(L.get("wv")), None,
-                                  *[int(ty.get(n, 0)) for n in PROJECTIONS])
+                                  *[int(ty.get(n, 0)) for n in PROJECTIONS], int(L["window"]))
         self._keep.append(arr)
         t = int(c.ggml_type)
         return Decoder(

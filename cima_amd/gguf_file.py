@@ -286,6 +286,12 @@ def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 25
         raise GGUFError("blk.0.attn_q.weight is missing -- not a qwen2 / llama-family decoder")
     eps = g.meta_float(f"{a}.attention.layer_norm_rms_epsilon")
     theta = g.meta_float(f"{a}.rope.freq_base")
+    # sliding-window attention: one window for every layer is supported; a
+    # per-layer pattern (alternating local / global layers) is not, and is
+    # refused rather than decoded with the wrong attention span
+    window = g.meta_int(f"{a}.attention.sliding_window") or 0
+    if window and any(k.startswith(f"{a}.attention.sliding_window_") for k in g.meta):
+        raise GGUFError(f"{a}: per-layer sliding-window patterns are not supported by this decoder")
     return DecoderConfig(
         n_layers=need("block_count"), hidden=hidden, q_heads=n_heads,
         kv_heads=g.meta_int(f"{a}.attention.head_count_kv") or n_heads,
@@ -293,7 +299,7 @@ def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 25
         ffn=need("feed_forward_length"), vocab=vocab,
         rope_theta=1e4 if theta is None else theta, rms_eps=1e-6 if eps is None else eps,
         qkv_bias="blk.0.attn_q.bias" in g.tensors, tied="output.weight" not in g.tensors,
-        ggml_type=q.ggml_type, max_seq=ms, attn_chunk=attn_chunk)
+        ggml_type=q.ggml_type, max_seq=ms, attn_chunk=attn_chunk, window=window)
 
 
 def _f16_vector(g: GGUFFile, name: str, n: int) -> np.ndarray:
@@ -369,6 +375,8 @@ def save_model(path: str, m, arch: str = "qwen2", alignment: int = 32) -> None:
             (f"{arch}.rope.freq_base", T_F32, c.rope_theta),
             (f"{arch}.attention.layer_norm_rms_epsilon", T_F32, c.rms_eps),
             (f"{arch}.vocab_size", T_U32, c.vocab)]
+    if c.window:
+        meta.append((f"{arch}.attention.sliding_window", T_U32, c.window))
     f32 = lambda a: np.asarray(a, np.float32).tobytes()  # noqa: E731
     ts = [("token_embd.weight", m.embed_type, (c.vocab, c.hidden), m.embed.tobytes()),
           ("output_norm.weight", GGML_F32, (c.hidden,), f32(m.final_norm))]

@@ -52,7 +52,8 @@ class DecoderLayer(ctypes.Structure):
     _fields_ = ([(n, ctypes.c_void_p) for n in (
         "attn_norm", "wqkv", "bqkv", "wo", "ffn_norm", "w_gate_up", "w_down", "k_cache", "v_cache", "wk", "wv",
         "w_up")]
-        + [(n, ctypes.c_int) for n in ("type_q", "type_k", "type_v", "type_o", "type_gate", "type_up", "type_down")])
+        + [(n, ctypes.c_int) for n in ("type_q", "type_k", "type_v", "type_o", "type_gate", "type_up", "type_down",
+                                       "window")])
 
 
 class Decoder(ctypes.Structure):
@@ -112,8 +113,8 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_kv_append.argtypes = [P, P, P, P, P, I, I, I, I, I, P]
     L.cima_hip_attn_decode_split.argtypes = [P, P, P, P, P, I, I, I, I, I, I, I, F, I, P]
     L.cima_hip_attn_reduce.argtypes = [P, P, P, I, I, I, I, I, I, I, P]
-    L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, I, I, I, I, I, I, F, F, P]
-    L.cima_hip_attn_gguf_gemv.argtypes = [P, I, P, I, I, I, I, I, P, P, P, P, I, I]
+    L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, I, I, I, I, I, I, F, F, I, P]
+    L.cima_hip_attn_gguf_gemv.argtypes = [P, I, P, I, I, I, I, I, I, P, P, P, P, I, I]
     L.cima_hip_gguf_gemv_argmax.argtypes = [P, I, P, P, F, P, P, I, I, P]
     L.cima_hip_argmax.argtypes = [P, P, P, I, F]
     L.cima_hip_argmax_to_ids.argtypes = [P, P, P, P]
@@ -375,17 +376,20 @@ class HipCtx:
                                                   seq, max_seq, window, _ptr(pos_dev)))
 
     def attn_decode(self, qkv, kc, vc, part, q_heads: int, kv_heads: int, dim: int, max_seq: int, csz: int,
-                    n_chunks: int, theta: float, scale: float, pos_dev) -> None:
-        """RoPE + KV append + split attention partials in one launch."""
+                    n_chunks: int, theta: float, scale: float, pos_dev, window: int = 0) -> None:
+        """RoPE + KV append + split attention partials in one launch
+        (window > 0: the last `window` positions only)."""
         self._check(self.lib.cima_hip_attn_decode(self.handle, _ptr(qkv), _ptr(kc), _ptr(vc), _ptr(part), q_heads,
-                                                  kv_heads, dim, max_seq, csz, n_chunks, theta, scale,
+                                                  kv_heads, dim, max_seq, csz, n_chunks, theta, scale, window,
                                                   _ptr(pos_dev)))
 
     def attn_gguf_gemv(self, fmt: int, part, q_heads: int, dim: int, csz: int, n_chunks: int, max_seq: int,
-                       pos_dev, w, bias, y, n: int, mode: int = 0) -> None:
-        """o projection of the attention merged from split partials (f16)."""
+                       pos_dev, w, bias, y, n: int, mode: int = 0, window: int = 0) -> None:
+        """o projection of the attention merged from split partials (f16;
+        window > 0: merged over the last `window` positions)."""
         self._check(self.lib.cima_hip_attn_gguf_gemv(self.handle, int(fmt), _ptr(part), q_heads, dim, csz, n_chunks,
-                                                     max_seq, _ptr(pos_dev), _ptr(w), _ptr(bias), _ptr(y), n, mode))
+                                                     max_seq, window, _ptr(pos_dev), _ptr(w), _ptr(bias), _ptr(y), n,
+                                                     mode))
 
     def gguf_gemv_argmax(self, fmt: int, x, norm_w, eps: float, w, y, n: int, k: int, slot) -> None:
         """Head GEMV (optional RMSNorm prologue) with the greedy argmax into slot."""

@@ -239,20 +239,25 @@ int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_
  * *pos_dev: RoPE of q and k from qkv = [q | k | v] (the fused q/k/v GEMV
  * output), append of the new k and v to the caches, and the split
  * attention of every (query head, chunk) into part (as for
- * cima_hip_attn_decode_split).  Replaces rope x2 + kv_append +
- * attn_decode_split (src/models/transformer.rs:1100-1160); the merge is
- * cima_hip_attn_reduce or, fused, cima_hip_attn_gguf_gemv. */
+ * cima_hip_attn_decode_split, window > 0 keeping the last `window`
+ * positions).  Replaces rope x2 + kv_append + attn_decode_split
+ * (src/models/transformer.rs:1100-1160; window as the split kernel's,
+ * src/kernels.cu:557-559); the merge is cima_hip_attn_reduce or, fused,
+ * cima_hip_attn_gguf_gemv with the same window.  Chunks past the position
+ * or wholly before the window write nothing. */
 int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* k_cache, void* v_cache, float* part, int q_heads,
                          int kv_heads, int dim, int max_seq, int csz, int n_chunks, float theta, float scale,
-                         const int* pos_dev);
+                         int window, const int* pos_dev);
 /* The o projection of merged attention: cima_hip_gguf_gemv (f16, mode 0 or
  * 1, k = q_heads * dim) whose x is merged, inside the GEMV, from the split
- * partials of the first *pos_dev + 1 positions: x[h*dim + d] =
- * f16(sum_c e^(m_c - M) acc_c[d] / sum_c e^(m_c - M) l_c).  Replaces
- * attn_reduce + gguf_gemv (src/models/transformer.rs:1161-1238). */
+ * partials of the first *pos_dev + 1 positions (window > 0: of the chunks
+ * from the window's first position on, as k_attn_reduce,
+ * src/kernels.cu:619-621): x[h*dim + d] = f16(sum_c e^(m_c - M) acc_c[d] /
+ * sum_c e^(m_c - M) l_c).  Replaces attn_reduce + gguf_gemv
+ * (src/models/transformer.rs:1161-1238). */
 int cima_hip_attn_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const float* part, int q_heads, int dim, int csz,
-                            int n_chunks, int max_seq, const int* pos_dev, const void* w, const void* bias, void* y,
-                            int n, int mode);
+                            int n_chunks, int max_seq, int window, const int* pos_dev, const void* w,
+                            const void* bias, void* y, int n, int mode);
 /* The head GEMV with the greedy argmax folded in: y = W . rmsnorm(x)
  * (norm_w NULL: W . x), f16, and *slot = max(*slot, argmax key of every
  * y[r]) with the key of cima_hip_argmax (no softcap).  *slot must be 0 on
@@ -294,6 +299,10 @@ typedef struct cima_decoder_layer {
     const void* wv;         /* [kv_heads * head_dim, hidden], or NULL */
     const void* w_up;       /* [ffn, hidden], or NULL */
     int type_q, type_k, type_v, type_o, type_gate, type_up, type_down;
+    /* sliding-window attention: > 0 keeps the last `window` positions
+     * (the reference's per-layer window, src/models/gemma4/mod.rs:1396-1421);
+     * 0 = full causal attention */
+    int window;
 } cima_decoder_layer;
 
 /* A decoder and its device workspace for cima_hip_decode_step. */

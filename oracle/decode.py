@@ -164,7 +164,7 @@ def _gemv(t, w, x, n, k, threads):
     return gguf_gemv_packed(t, w, np.asarray(x, np.float32), n, k, threads=threads).astype(np.float64)
 
 
-def decode_step(m: dict, token: int, pos: int, threads: int = 8):
+def decode_step(m: dict, token: int, pos: int, threads: int = 8, trace: list | None = None):
     """One greedy decode step of a Qwen2-shaped model held in numpy.
 
     ``m``: cfg (dict with hidden, q_heads, kv_heads, head_dim, ffn, vocab,
@@ -177,7 +177,11 @@ def decode_step(m: dict, token: int, pos: int, threads: int = 8):
     where the reference writes f16 activations: the gathered x, the normed
     h, q/k/v after the bias add (rounded twice: GEMV output, then bias),
     q/k after RoPE, the attention output, x after each residual add, the
-    SwiGLU gate/up/product and the logits.
+    SwiGLU gate/up/product and the logits.  A layer's optional ``window`` >
+    0 keeps its last `window` positions (the split kernel's window,
+    src/kernels.cu:557-559).  With ``trace`` a list, each layer appends
+    {"attn": x after the attention residual, "ffn": x after the FFN
+    residual} (f16).
 
     Returns (logits f16 [vocab], next token).
     """
@@ -202,13 +206,16 @@ def decode_step(m: dict, token: int, pos: int, threads: int = 8):
         k = rope(qkv[qd:qd + kvd].reshape(1, kvh, hd), pos, c["rope_theta"])
         v = qkv[qd + kvd:].reshape(1, kvh, hd)
         kv_append(L["k_cache"], L["v_cache"], k, v, pos)
-        att = f16(attention(q, L["k_cache"], L["v_cache"], pos + 1, scale)).reshape(-1)
+        att = f16(attention(q, L["k_cache"], L["v_cache"], pos + 1, scale, L.get("window", 0))).reshape(-1)
         x = f16(x.astype(np.float64) + _gemv(ty["o"], L["wo"], att, hid, qd, threads))
+        x_attn = x
         h = rmsnorm(x, L["ffn_norm"], eps)[0]
         gu = _gemv(ty["gate"], L["w_gate_up"], h, 2 * ffn, hid, threads)
         g, u = f16(gu[:ffn]).astype(np.float64), f16(gu[ffn:]).astype(np.float64)
         act = f16(g / (1.0 + np.exp(-g)) * u)
         x = f16(x.astype(np.float64) + _gemv(ty["down"], L["w_down"], act, hid, ffn, threads))
+        if trace is not None:
+            trace.append({"attn": x_attn, "ffn": x})
     h = rmsnorm(x, m["final_norm"], eps)[0]
     head = m.get("head")
     ht = c.get("head_type", c["embed_type"]) if head is not None else c["embed_type"]

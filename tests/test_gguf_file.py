@@ -208,3 +208,21 @@ def test_oracle_split_qkv_equals_fused():
     b = od.decode_step(split, 7, 50, threads=2)
     assert np.array_equal(a[0], b[0]) and a[1] == b[1]
     assert oracle.BLOCK_ELEMS[Q8_0] == 32
+
+
+def test_sliding_window_metadata(tmp_path):
+    """A single sliding window in the metadata reaches the decoder config;
+    a per-layer window pattern is refused."""
+    from cima_amd.decoder import DecoderConfig, synthetic_model
+
+    cfg = DecoderConfig(n_layers=1, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=100,
+                        max_seq=256, window=96)
+    m = synthetic_model(cfg, seed=2)
+    path = str(tmp_path / "win.gguf")
+    gf.save_model(path, m)
+    g = gf.GGUFFile(path)
+    assert gf.decoder_config(g).window == 96
+    g.meta["qwen2.attention.sliding_window_pattern"] = 2
+    with pytest.raises(gf.GGUFError):
+        gf.decoder_config(g)
+    g.close()

@@ -5,10 +5,13 @@ reference's decode order.
 
 Tolerances: element ops on f16 data are held to one or two f16 ulps of the
 float64 oracle (|d| <= 2^-9 |v| + small absolute slack for RoPE's fp32
-angles); GEMVs to the north star's 1e-3 normwise relative error; a full
-step's logits to 1e-2 normwise (two dozen chained f16 roundings, each a
-possible ulp apart) with the greedy token equal unless the oracle's top two
-logits are within that tolerance."""
+angles); GEMVs to the north star's 1e-3 normwise relative error; each
+layer of a full step, fed the oracle's residual stream, to 1e-3 normwise
+after its attention and after its FFN half; a full step's logits to
+2 sqrt(layers) * 1e-3 normwise (those per-layer errors added in
+quadrature, x2 for amplification through later layers; at config 5 the
+quadrature sum of the measured per-layer errors, x4) with the greedy token equal unless the oracle's top two logits are within
+that tolerance."""
 import numpy as np
 import pytest
 
@@ -176,13 +179,19 @@ def test_attn_split_and_reduce(hip, dim, qh, kvh, seq, csz, window):
 
 
 @pytest.mark.parametrize("fill", ["zero", "nan"])
-@pytest.mark.parametrize("dim,qh,kvh,pos,csz", [(64, 14, 2, 2048, 256), (64, 14, 2, 0, 256), (128, 32, 8, 300, 128),
-                                                (64, 14, 2, 255, 256), (64, 14, 2, 256, 256), (64, 14, 2, 1000, 64)])
-def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz, fill):
+@pytest.mark.parametrize("dim,qh,kvh,pos,csz,window", [
+    (64, 14, 2, 2048, 256, 0), (64, 14, 2, 0, 256, 0), (128, 32, 8, 300, 128, 0), (64, 14, 2, 255, 256, 0),
+    (64, 14, 2, 256, 256, 0), (64, 14, 2, 1000, 64, 0), (64, 28, 2, 700, 256, 0), (128, 4, 4, 999, 256, 0),
+    (64, 14, 2, 2048, 256, 700), (64, 14, 2, 1000, 64, 300), (128, 32, 8, 300, 128, 200),
+    (64, 14, 2, 600, 256, 1)])
+def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz, window, fill):
     """rope q, k + append + split in one launch, merged by attn_reduce, ==
     the separate ops; and the merge folded into the o-projection GEMV.  The
     cache rows past the position and the partials buffer start as zeros or
-    as NaN: the kernels load them speculatively and must not let them in."""
+    as NaN: the kernels load them speculatively and must not let them in.
+    GQA groups of 1, 4, 7 and 14 query heads per kv head (more than one
+    head group per workgroup); window > 0 keeps the last `window`
+    positions in the split, the reduce and the merge inside the GEMV."""
     max_seq = 4096
     nch = max_seq // csz
     r = np.random.default_rng(pos + dim)
@@ -196,14 +205,14 @@ def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz, fill):
     out = torch.empty((qh, dim), dtype=torch.float16, device="cuda")
     posd = torch.tensor([pos], dtype=torch.int32, device="cuda")
     scale = 1 / np.sqrt(dim)
-    hip.attn_decode(dev16(qkv), dkc, dvc, part, qh, kvh, dim, max_seq, csz, nch, 1e6, scale, posd)
-    hip.attn_reduce(part, out, qh, dim, csz, nch, 0, max_seq, 0, posd)
+    hip.attn_decode(dev16(qkv), dkc, dvc, part, qh, kvh, dim, max_seq, csz, nch, 1e6, scale, posd, window)
+    hip.attn_reduce(part, out, qh, dim, csz, nch, 0, max_seq, window, posd)
     q = od.rope(qkv[:qh * dim].reshape(1, qh, dim), pos, 1e6)[0]
     k = od.rope(qkv[qh * dim:(qh + kvh) * dim].reshape(1, kvh, dim), pos, 1e6)
     v = qkv[(qh + kvh) * dim:].reshape(1, kvh, dim)
     wk, wv = kc.copy(), vc.copy()
     od.kv_append(wk, wv, k, v, pos)
-    want = od.attention(q, wk, wv, pos + 1, scale)
+    want = od.attention(q, wk, wv, pos + 1, scale, window)
     got = host(out).astype(np.float64)
     assert np.max(np.abs(got - want)) <= 3e-3, np.max(np.abs(got - want))
     gk = host(dkc)
@@ -216,7 +225,8 @@ def test_attn_decode_fused(hip, dim, qh, kvh, pos, csz, fill):
     w = synth.weights(Q8_0, 40 + dim, 0.02, n, qh * dim)
     y0 = synth.normal(41, 1.0, n).astype(np.float16)
     y = dev16(y0)
-    hip.attn_gguf_gemv(Q8_0, part, qh, dim, csz, nch, max_seq, posd, torch.from_numpy(w).cuda(), None, y, n, 1)
+    hip.attn_gguf_gemv(Q8_0, part, qh, dim, csz, nch, max_seq, posd, torch.from_numpy(w).cuda(), None, y, n, 1,
+                       window)
     att = host(out).reshape(-1)  # the merged attention, f16
     ref = y0.astype(np.float64) + oracle.gguf_gemv_packed(Q8_0, w, att.astype(np.float32), n, qh * dim)
     r_ = rel(host(y), ref)
@@ -302,6 +312,18 @@ def _oracle_model(m, kvs):
                 layers=[dict(L, k_cache=kv[0].copy(), v_cache=kv[1].copy()) for L, kv in zip(m.layers, kvs)])
 
 
+# End-to-end logits bound of a decode step: every layer is held to 1e-3
+# normwise against the oracle on the oracle's own input
+# (test_decode_step_config5_per_layer); independent per-layer errors add in
+# quadrature through the residual stream, and later layers amplify an
+# earlier layer's error (measured at config 5: the end-to-end error is 2.6x
+# the quadrature sum of the measured per-layer errors, which sit at about
+# half the bar), allowed for by a factor 2 on the bar: 2 sqrt(L) * 1e-3
+# (9.8e-3 at config 5's 24 layers, 2.8e-3 at 2).
+def E2E_TOL(n_layers, per_layer=1e-3):
+    return 2.0 * float(np.sqrt(n_layers)) * per_layer
+
+
 def _check_step(logits_gpu, tok_gpu, logits_ref, tok_ref, tol):
     r = rel(logits_gpu, logits_ref)
     top = np.sort(logits_ref.astype(np.float64))[-2:]
@@ -326,7 +348,7 @@ def test_decode_steps_small_against_oracle(hip):
         torch.cuda.synchronize()
         lg = host(d.logits)
         ref_logits, ref_tok = od.decode_step(om, tok, pos)
-        _check_step(lg, d.token(), ref_logits, ref_tok, 1e-2)
+        _check_step(lg, d.token(), ref_logits, ref_tok, E2E_TOL(SMALL.n_layers))
         assert d.position() == pos + 1
         # continue both from the GPU's token so the trajectories stay aligned
         tok, pos = d.token(), pos + 1
@@ -368,7 +390,7 @@ def test_decode_step_config5_full_size(hip):
     d.replay()
     torch.cuda.synchronize()
     ref_logits, ref_tok = od.decode_step(_oracle_model(m, kvs), 1234, 2048, threads=16)
-    _check_step(host(d.logits), d.token(), ref_logits, ref_tok, 1e-2)
+    _check_step(host(d.logits), d.token(), ref_logits, ref_tok, E2E_TOL(cfg.n_layers))
     assert d.position() == 2049
 
 
@@ -414,7 +436,92 @@ def test_decode_step_mixed_formats_from_gguf(hip, tmp_path):
         gd.replay()
         torch.cuda.synchronize()
         ref_logits, ref_tok = od.decode_step(om, tok, pos)
-        _check_step(host(d.logits), d.token(), ref_logits, ref_tok, 1e-2)
+        _check_step(host(d.logits), d.token(), ref_logits, ref_tok, E2E_TOL(m.cfg.n_layers))
         assert np.all(host(d.logits) == host(gd.logits)) and d.token() == gd.token()
         tok, pos = d.token(), pos + 1
     g.close()
+
+
+def _layer_teacher_forced(hip, d, L, x_in, cfg, pos_dev):
+    """One decoder layer on the GPU through the decode step's own entry
+    points, from the given residual x_in (f16): returns (x after the
+    attention residual, x after the FFN residual), f16."""
+    qd, kvd = cfg.q_heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    csz = cfg.attn_chunk
+    nch = -(-cfg.max_seq // csz)
+    t = int(cfg.ggml_type)
+    d.x.copy_(torch.from_numpy(np.ascontiguousarray(x_in, np.float16)).cuda())
+    hip.rmsnorm_gguf_gemv(t, d.x, L["attn_norm"], cfg.rms_eps, L["wqkv"], L["bqkv"], d.qkv, qd + 2 * kvd,
+                          cfg.hidden, 0)
+    hip.attn_decode(d.qkv, L["k_cache"], L["v_cache"], d.part, cfg.q_heads, cfg.kv_heads, cfg.head_dim,
+                    cfg.max_seq, csz, nch, cfg.rope_theta, 1 / np.sqrt(cfg.head_dim), pos_dev, L["window"])
+    hip.attn_gguf_gemv(t, d.part, cfg.q_heads, cfg.head_dim, csz, nch, cfg.max_seq, pos_dev, L["wo"], None, d.x,
+                       cfg.hidden, 1, L["window"])
+    xa = host(d.x).copy()
+    hip.rmsnorm_gguf_gemv(t, d.x, L["ffn_norm"], cfg.rms_eps, L["w_gate_up"], None, d.act, cfg.ffn, cfg.hidden, 2)
+    hip.gguf_gemv(t, d.act, L["w_down"], None, d.x, cfg.hidden, cfg.ffn, 1)
+    return xa, host(d.x).copy()
+
+
+@pytest.mark.parametrize("window", [0, 700], ids=["full", "window700"])
+def test_decode_step_config5_per_layer(hip, window):
+    """Config 5 at full size, layer by layer: every layer is fed the
+    oracle's residual stream and its two outputs (x after the attention
+    residual, x after the FFN residual) must be within 1e-3 normwise of the
+    oracle's (oracle/decode.py, f16 activations where the reference writes
+    them), so a drift is pinned to its layer and half.  Then the whole
+    step's logits, through the fused decode step, against the oracle."""
+    cfg = DecoderConfig(window=window)
+    m = synthetic_model(cfg, seed=5)
+    kvs = [synthetic_kv(cfg, i, 2048) for i in range(cfg.n_layers)]
+    om = _oracle_model(m, kvs)
+    trace = []
+    ref_logits, ref_tok = od.decode_step(om, 1234, 2048, threads=16, trace=trace)
+    d = DeviceDecoder(hip, m)
+    for i, (kc, vc) in enumerate(kvs):
+        d.load_kv(i, kc, vc)
+    posd = torch.tensor([2048], dtype=torch.int32, device="cuda")
+    x_in = oracle.gather(int(m.embed_type), m.embed, np.array([1234], np.uint32), cfg.hidden).view(np.float16)[0]
+    worst, sq = 0.0, 0.0
+    for i, L in enumerate(d.layers):
+        xa, xf = _layer_teacher_forced(hip, d, L, x_in, cfg, posd)
+        ra = rel(xa.astype(np.float64), trace[i]["attn"])
+        rf = rel(xf.astype(np.float64), trace[i]["ffn"])
+        worst = max(worst, ra, rf)
+        sq += rf * rf
+        assert ra <= 1e-3 and rf <= 1e-3, (i, ra, rf)
+        x_in = trace[i]["ffn"]
+    print(f"config 5 per layer (window {window}): worst rel {worst:.2e}")
+    # the fused step end to end (fresh caches)
+    d2 = DeviceDecoder(hip, m)
+    for i, (kc, vc) in enumerate(kvs):
+        d2.load_kv(i, kc, vc)
+    d2.set_state(1234, 2048)
+    d2.step()
+    torch.cuda.synchronize()
+    # the bound from this model's own measured per-layer errors (their
+    # quadrature sum, x4 for amplification through later layers: 2.6x
+    # measured), never looser than the generic one
+    tol = min(E2E_TOL(cfg.n_layers), 4.0 * float(np.sqrt(sq)) + 2.0 ** -11)
+    _check_step(host(d2.logits), d2.token(), ref_logits, ref_tok, tol)
+
+
+def test_decode_steps_window_small(hip):
+    """A sliding window shorter than the context, through the fused decode
+    step over several steps, against the oracle."""
+    cfg = DecoderConfig(n_layers=2, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                        max_seq=512, window=100, attn_chunk=64)
+    m = synthetic_model(cfg, seed=8)
+    kvs = [synthetic_kv(cfg, i, 300) for i in range(cfg.n_layers)]
+    d = DeviceDecoder(hip, m)
+    for i, (kc, vc) in enumerate(kvs):
+        d.load_kv(i, kc, vc)
+    om = _oracle_model(m, kvs)
+    tok, pos = 17, 300
+    d.set_state(tok, pos)
+    for s in range(3):
+        d.step()
+        torch.cuda.synchronize()
+        ref_logits, ref_tok = od.decode_step(om, tok, pos)
+        _check_step(host(d.logits), d.token(), ref_logits, ref_tok, E2E_TOL(cfg.n_layers))
+        tok, pos = d.token(), pos + 1
