@@ -184,7 +184,6 @@ def main():
     read_us = {}
     hot_us = {}
     gemm_flops = {}
-    gemm_route = {}
     # the roofline kernel: fused gate+up SwiGLU, cold over the 32 layers
     pair_bytes = 2 * wbytes(Q4_K, FFN, HID) + 4 * HID + 4 * FFN
     pair_us = time_calls(lambda L: ctx.gguf_gemv_swiglu(Q4_K, h, L["gate"], L["up"], None, None, act, FFN, HID),
@@ -265,13 +264,12 @@ def main():
         # config 4: prefill dequant-GEMM on MFMA, Q4_K 14336x4096, X bf16 (m tokens), Y fp32
         gw = synth.weights(Q4_K, 300, 0.02, FFN, HID)
         gbufs = [torch.from_numpy(gw).to(dev) for _ in range(12)]
-        # the prefill route of the engine (cima_hip_gguf_gemm_slab): fused MFMA
-        # kernel or dequant into this slab + hipBLASLt, whichever its rule picks
-        gslab = torch.empty(ctx.gemm_slab_bytes(512, FFN, HID), dtype=torch.uint8, device=dev)
+        # the prefill entry point of the engine (cima_hip_gguf_gemm_slab, with
+        # the reference's 32 MiB scratch): the fused MFMA kernels
+        gslab = torch.empty(32 << 20, dtype=torch.uint8, device=dev)
         for m in (16, 128, 512):
             gx = torch.from_numpy(synth.normal(301, 1.0, m * HID)).to(dev).to(torch.bfloat16).reshape(m, HID)
             gy = torch.empty((m, FFN), device=dev)
-            gemm_route[m] = ctx.gguf_gemm_slab(Q4_K, gx, gbufs[0], gy, m, FFN, HID, gslab)
             us = time_calls(lambda b: ctx.gguf_gemm_slab(Q4_K, gx, b, gy, m, FFN, HID, gslab), gbufs, calls=24)
             b = wbytes(Q4_K, FFN, HID) + 2 * m * HID + 4 * m * FFN
             per_shape[f"q4_k gemm 14336x4096 m={m} (config 4)"] = (us, b)
@@ -292,8 +290,7 @@ def main():
         if name in gemm_flops:
             tf = gemm_flops[name] / us / 1e6
             shapes_out[name].update({"tflop_s": round(tf, 1), "mfma_frac_f16_dense": round(tf / 2500.0, 4)})
-            m = int(name.split("m=")[1].split()[0])
-            shapes_out[name]["route"] = "dequant slab + hipBLASLt" if gemm_route.get(m) else "fused MFMA"
+            shapes_out[name]["route"] = "fused MFMA"
 
     achieved = pair_bytes / pair_us / 1e3
     traffic = None

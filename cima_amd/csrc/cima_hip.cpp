@@ -119,12 +119,9 @@ struct cima_hip_ctx {
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
-    int gemm_lib_min = 0;     // dequant-slab prefill: fewest tokens routed to the library GEMM (0 = built-in rule)
-    int last_gemm_route = 0;  // route of the last gguf_gemm_slab call: 0 fused MFMA kernel, 1 slab + library
-    int gemm_autotune = 0;    // time hipBLASLt's candidates on a shape's first library call
     void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
     // cached library plans: (m, n, k, y dtype, workspace cap) -> plan
-    std::map<std::tuple<int, int, int, int, size_t>, struct LtPlan*> lt_plans;
+    std::map<std::tuple<int, int, int, int, int, size_t>, struct LtPlan*> lt_plans;
 };
 
 namespace {
@@ -527,7 +524,6 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
-    if (const char* s = getenv("CIMA_GEMM_AUTOTUNE")) ctx->gemm_autotune = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -749,9 +745,9 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // builds (once per shape) the hipBLASLt descriptors and the algorithm the
 // library's heuristic ranks first for them
-int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, LtPlan** out) {
+int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int ldd, int y_dtype, size_t ws_cap, LtPlan** out) {
     const LtApi& L = lt_api();
-    auto key = std::make_tuple(m, n, k, y_dtype, ws_cap);
+    auto key = std::make_tuple(m, n, k, ldd, y_dtype, ws_cap);
     auto it = ctx->lt_plans.find(key);
     if (it != ctx->lt_plans.end()) {
         *out = it->second;
@@ -760,7 +756,7 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, 
     if (!ctx->lt) {
         hipblasLtHandle_t h = nullptr;
         if (L.create(&h) != HIPBLAS_STATUS_SUCCESS)
-            return fail(CIMA_E_LIBRARY, "cima_hip_gguf_gemm_slab: hipblasLtCreate failed");
+            return fail(CIMA_E_LIBRARY, "cima_hip_nf4_gemm_slab: hipblasLtCreate failed");
         ctx->lt = h;
     }
     LtPlan* p = new LtPlan();
@@ -772,7 +768,7 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, 
               L.desc_set(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
               L.layout_create(&p->a, HIP_R_16F, (uint64_t)k, (uint64_t)n, k) == HIPBLAS_STATUS_SUCCESS &&
               L.layout_create(&p->b, HIP_R_16F, (uint64_t)k, (uint64_t)m, k) == HIPBLAS_STATUS_SUCCESS &&
-              L.layout_create(&p->d, yt, (uint64_t)n, (uint64_t)m, n) == HIPBLAS_STATUS_SUCCESS;
+              L.layout_create(&p->d, yt, (uint64_t)n, (uint64_t)m, ldd) == HIPBLAS_STATUS_SUCCESS;
     if (ok) {
         hipblasLtMatmulPreference_t pref = nullptr;
         uint64_t cap = ws_cap;
@@ -799,46 +795,6 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int y_dtype, size_t ws_cap, 
     return 0;
 }
 
-// Times each heuristic candidate of the plan on the call's own operands
-// (one warm-up and three timed runs, HIP events on the context stream; the
-// host waits) and keeps the fastest.  y receives results that the call's
-// own GEMM then overwrites.  Skipped while the stream is being captured.
-void lt_autotune(cima_hip_ctx* ctx, LtPlan* p, const void* wh, const void* xh, void* y, void* ws) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
-    p->tuned = true;
-    if (p->ncand < 2) return;
-    hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-        if (e0) (void)hipEventDestroy(e0);
-        return;
-    }
-    const LtApi& L = lt_api();
-    const float alpha = 1.f, beta = 0.f;
-    float best = 0.f;
-    int best_i = 0;
-    for (int i = 0; i < p->ncand; i++) {
-        auto run = [&] {
-            return L.matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y, p->d, y, p->d,
-                            &p->cand[i], p->cand_ws[i] ? ws : nullptr, p->cand_ws[i], ctx->stream) ==
-                   HIPBLAS_STATUS_SUCCESS;
-        };
-        bool ok = run() && hipEventRecord(e0, ctx->stream) == hipSuccess;
-        for (int r = 0; ok && r < 3; r++) ok = run();
-        float ms = 0.f;
-        ok = ok && hipEventRecord(e1, ctx->stream) == hipSuccess && hipEventSynchronize(e1) == hipSuccess &&
-             hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
-        if (ok && (i == 0 || ms < best || best == 0.f)) {
-            best = ms;
-            best_i = i;
-        }
-    }
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    p->algo = p->cand[best_i];
-    p->ws = p->cand_ws[best_i];
-}
-
 // rounds X (f32 or bf16, m*k elements, m*k % 8 == 0) to f16 at dst
 int x_to_f16(cima_hip_ctx* ctx, const void* x, void* dst, long long elems, int x_dtype, const char* api) {
     hipFunction_t f;
@@ -853,15 +809,14 @@ int x_to_f16(cima_hip_ctx* ctx, const void* x, void* dst, long long elems, int x
 // Y[m, n] (ld n) = Xh[m, k] . Wh[n, k]^T through hipBLASLt, f16 operands,
 // fp32 accumulation; *ran = false (nothing launched) when the library is
 // absent or has no algorithm for the shape within ws_cap bytes of workspace
-int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, int n, int k, int y_dtype, void* ws,
-            size_t ws_cap, const char* api, bool* ran) {
+int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, int n, int k, int ldd, int y_dtype,
+            void* ws, size_t ws_cap, const char* api, bool* ran) {
     *ran = false;
     if (!lt_api().ok) return 0;
     LtPlan* p = nullptr;
-    if (int rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p)) return rc;
+    if (int rc = lt_plan(ctx, m, n, k, ldd, y_dtype, ws_cap, &p)) return rc;
     if (!p->ok) return 0;
     const float alpha = 1.f, beta = 0.f;
-    if (ctx->gemm_autotune && !p->tuned) lt_autotune(ctx, p, wh, xh, y, ws);
     hipblasStatus_t st = lt_api().matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y,
                                          p->d, y, p->d, &p->algo, p->ws ? ws : nullptr, p->ws, ctx->stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);
@@ -869,73 +824,21 @@ int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, i
     return 0;
 }
 
-// Built-in route of cima_hip_gguf_gemm_slab.  Measured on MI355X (Q4_K,
-// bf16 X, fp32 Y, cold weights; fused / slab + hipBLASLt in us):
-//   14336x4096  m=16 18/54   m=64 36/56   m=128 47/65   m=256 73/76  m=384 110/82
-//   4096x14336  m=16 43/54   m=48 106/61  m=128 106/91  m=256 206/91
-//   4096x4096   m=16 15/33   m=48 33/34   m=128 33/42   m=192 64/47  m=256 64/39
-//   1024x4096   m=16 13/19   m=48 32/19   m=256 63/25
-//   6144x4096   m=48 34/40   m=128 34/44  m=192 65/50
-// The split-k 16-token tiles win up to 32 tokens everywhere.  The 32-, 64-
-// and 128-token tiles give one workgroup per 128 weight rows and token tile, and
-// a narrow grid of long rows leaves most CUs idle: the slab route wins
-// there, and past 256 tokens, where the per-tile weight decode dominates.
-bool slab_route_pays(int m, int n, int k, int num_cu) {
-    if (m <= 32) return false;
-    if (m > 256) return true;
-    const int bn = fused_bn(m, n, num_cu);
-    const long long wgs = (long long)((n + 127) / 128) * ((m + bn - 1) / bn);
-    return wgs * 4096 < (long long)(bn <= 64 ? 48 : 160) * k;
-}
-
-size_t ws_cap_of(size_t rest) { return rest < kLtWorkspaceMax ? rest & ~(size_t)255 : kLtWorkspaceMax; }
 
 }  // namespace
 
 int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, int m, int n, int k,
                             int ldy, int x_dtype, int y_dtype, void* slab, unsigned long long slab_bytes) {
     const char* api = "cima_hip_gguf_gemm_slab";
-    if (ctx) ctx->last_gemm_route = 0;
     const Fmt* F = nullptr;
     int rc = gemm_check(ctx, t, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api, &F);
     if (rc || !F) return rc;
     if (slab_bytes && (!slab || !aligned(slab, 256)))
         return fail(CIMA_E_INVALID, "%s: slab must be a non-null 256-byte aligned device pointer", api);
-    // slab layout: W as f16 [n, k] | X as f16 [m, k] (unless X is f16) | workspace
-    const size_t wbytes = align256((size_t)n * k * 2);
-    const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
-    const bool lib = ctx->gemm_lib_min > 0 ? m >= ctx->gemm_lib_min : slab_route_pays(m, n, k, ctx->num_cu);
-    if (!lib || ldy != n || slab_bytes < wbytes + xbytes || !lt_api().ok)
-        return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
-    // the library route is taken only if hipBLASLt has a plan for the shape:
-    // ask before decoding anything
-    const size_t ws_cap = ws_cap_of((size_t)slab_bytes - wbytes - xbytes);
-    LtPlan* p = nullptr;
-    if ((rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p))) return rc;
-    if (!p->ok) return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
-    uint8_t* base = static_cast<uint8_t*>(slab);
-    // W rows are whole blocks laid end to end: one flat run decodes to [n, k]
-    if ((rc = cima_hip_gguf_dequant(ctx, t, w, base, (long long)n * (k / F->block_elems)))) return rc;
-    const void* xh = x;
-    if (x_dtype != CIMA_DT_F16) {
-        if ((rc = x_to_f16(ctx, x, base + wbytes, (long long)m * k, x_dtype, api))) return rc;
-        xh = base + wbytes;
-    }
-    bool ran = false;
-    if ((rc = lt_gemm(ctx, base, xh, y, m, n, k, y_dtype, base + wbytes + xbytes, ws_cap, api, &ran))) return rc;
-    if (!ran) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt plan vanished", api);
-    ctx->last_gemm_route = 1;
-    return 0;
+    // the fused kernels dequantise W tile by tile: the slab is not needed
+    return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
 }
 
-int cima_hip_set_gemm_route(cima_hip_ctx* ctx, int min_tokens) {
-    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemm_route: null context");
-    if (min_tokens < 0) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_route: %d < 0", min_tokens);
-    ctx->gemm_lib_min = min_tokens;
-    return 0;
-}
-
-int cima_hip_last_gemm_route(cima_hip_ctx* ctx) { return ctx ? ctx->last_gemm_route : -1; }
 
 int cima_hip_gguf_dequant(cima_hip_ctx* ctx, int t, const void* src, void* out, long long nblocks) {
     if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "cima_hip_gguf_dequant: context is not initialised");
@@ -1433,25 +1336,52 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
     if (!x || !packed || !absmax || !qmap || !y || !slab) return fail(CIMA_E_INVALID, "%s: null pointer", api);
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(slab, 256))
         return fail(CIMA_E_INVALID, "%s: misaligned x (16 B), y (4 B) or slab (256 B)", api);
-    const size_t wbytes = align256((size_t)n * k * 2);
+    // slab layout: [X as f16, unless it is f16][one row slice of W as f16][workspace]
+    // W is decoded and multiplied a row slice at a time (the reference's
+    // lin_gemm works through its 32 MiB DQ_SCRATCH the same way,
+    // src/models/transformer.rs:630-653), each slice's product written to
+    // its columns of Y (leading dimension n).  Slices start on absmax block
+    // boundaries: g rows is the smallest count whose elements are whole blocks.
     const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
-    if (slab_bytes < wbytes + xbytes)
-        return fail(CIMA_E_INVALID, "%s: slab of %llu bytes is smaller than the %zu the f16 W and X need", api,
-                    slab_bytes, wbytes + xbytes);
+    long long g = blocksize;
+    {
+        long long a = blocksize, b = k;
+        while (b) {
+            const long long t2 = a % b;
+            a = b;
+            b = t2;
+        }
+        g = blocksize / a;  // blocksize / gcd(blocksize, k)
+    }
+    const size_t rest = slab_bytes > xbytes ? (size_t)slab_bytes - xbytes : 0;
+    size_t ws_cap = rest / 8 < kLtWorkspaceMax ? (rest / 8) & ~(size_t)255 : kLtWorkspaceMax;
+    long long rows = (long long)((rest - ws_cap) / (2ULL * (size_t)k)) / g * g;
+    if (rows > n) rows = n;
+    if (rows < 1)
+        return fail(CIMA_E_INVALID, "%s: slab of %llu bytes holds no %lld-row slice of the f16 weight (k=%d)", api,
+                    slab_bytes, g, k);
     if (!lt_api().ok) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt (libhipblaslt.so.1) could not be opened", api);
-    const size_t ws_cap = ws_cap_of((size_t)slab_bytes - wbytes - xbytes);
-    LtPlan* p = nullptr;
-    int rc = lt_plan(ctx, m, n, k, y_dtype, ws_cap, &p);
-    if (rc) return rc;
-    if (!p->ok) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt offers no algorithm for m=%d n=%d k=%d", api, m, n, k);
     uint8_t* base = static_cast<uint8_t*>(slab);
-    if ((rc = cima_hip_nf4_dequant(ctx, packed, absmax, qmap, base, (long long)n * k, blocksize))) return rc;
+    uint8_t* wslab = base + xbytes;
+    void* ws = wslab + align256((size_t)rows * k * 2);
+    int rc = 0;
     const void* xh = x;
     if (x_dtype != CIMA_DT_F16) {
-        if ((rc = x_to_f16(ctx, x, base + wbytes, (long long)m * k, x_dtype, api))) return rc;
-        xh = base + wbytes;
+        if ((rc = x_to_f16(ctx, x, base, (long long)m * k, x_dtype, api))) return rc;
+        xh = base;
     }
-    bool ran = false;
-    if ((rc = lt_gemm(ctx, base, xh, y, m, n, k, y_dtype, base + wbytes + xbytes, ws_cap, api, &ran))) return rc;
-    return ran ? 0 : fail(CIMA_E_LIBRARY, "%s: hipBLASLt plan vanished", api);
+    const int yes = y_dtype == CIMA_DT_F32 ? 4 : 2;
+    for (long long r0 = 0; r0 < n; r0 += rows) {
+        const int nr = (int)std::min(rows, (long long)n - r0);
+        const long long e0 = r0 * k;
+        if ((rc = cima_hip_nf4_dequant(ctx, static_cast<const uint8_t*>(packed) + e0 / 2, absmax + e0 / blocksize,
+                                       qmap, wslab, (long long)nr * k, blocksize)))
+            return rc;
+        bool ran = false;
+        if ((rc = lt_gemm(ctx, wslab, xh, static_cast<uint8_t*>(y) + (size_t)r0 * yes, m, nr, k, n, y_dtype, ws,
+                          ws_cap, api, &ran)))
+            return rc;
+        if (!ran) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt offers no algorithm for m=%d n=%d k=%d", api, m, nr, k);
+    }
+    return 0;
 }

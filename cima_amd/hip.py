@@ -36,8 +36,7 @@ EXPORTS = (
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
     "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
-    "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_set_gemm_route",
-    "cima_hip_last_gemm_route", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
+    "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
     "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
@@ -132,8 +131,6 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_gguf_gemv_swiglu.argtypes = [P, I, P, P, P, P, P, P, I, I, I]
     L.cima_hip_gguf_gemm.argtypes = [P, I, P, P, P, I, I, I, I, I, I]
     L.cima_hip_gguf_gemm_slab.argtypes = [P, I, P, P, P, I, I, I, I, I, I, P, ctypes.c_ulonglong]
-    L.cima_hip_set_gemm_route.argtypes = [P, I]
-    L.cima_hip_last_gemm_route.argtypes = [P]
     L.cima_hip_gguf_dequant.argtypes = [P, I, P, P, LL]
     L.cima_hip_gguf_gather.argtypes = [P, I, P, P, P, I, I]
     _lib = L
@@ -272,30 +269,24 @@ class HipCtx:
         self._check(self.lib.cima_hip_gguf_gemm(self.handle, int(fmt), _ptr(x), _ptr(w), _ptr(y), m, n, k,
                                                 n if ldy is None else ldy, xd, yd))
 
-    def gguf_gemm_slab(self, fmt: int, x, w, y, m: int, n: int, k: int, slab, slab_bytes: Optional[int] = None,
+    def gguf_gemm_slab(self, fmt: int, x, w, y, m: int, n: int, k: int, slab=None, slab_bytes: Optional[int] = None,
                        ldy: Optional[int] = None, x_dtype: Optional[int] = None,
-                       y_dtype: Optional[int] = None) -> int:
-        """The same product through the reference's prefill route: from
-        ``set_gemm_route`` tokens up (by default where the built-in rule finds it faster) W is decoded into the
-        f16 ``slab`` and multiplied by the library GEMM; fewer tokens run the
-        fused kernel.  Returns the route taken (0 fused, 1 slab + library)."""
+                       y_dtype: Optional[int] = None) -> None:
+        """The same product through the reference's lin_gemm signature (the
+        engine's scratch slab is accepted and left untouched: the fused
+        kernels never expand W)."""
         xd, yd = self._gemm_dtypes(x, y, x_dtype, y_dtype)
         if slab_bytes is None:
-            slab_bytes = slab.numel() * slab.element_size()
+            slab_bytes = 0 if slab is None else slab.numel() * slab.element_size()
         self._check(self.lib.cima_hip_gguf_gemm_slab(self.handle, int(fmt), _ptr(x), _ptr(w), _ptr(y), m, n, k,
                                                      n if ldy is None else ldy, xd, yd, _ptr(slab),
                                                      int(slab_bytes)))
-        return int(self.lib.cima_hip_last_gemm_route(self.handle))
-
-    def set_gemm_route(self, min_tokens: int = 0) -> None:
-        """Fewest tokens ``gguf_gemm_slab`` sends to the library GEMM (0 = built-in rule)."""
-        self._check(self.lib.cima_hip_set_gemm_route(self.handle, int(min_tokens)))
 
     @staticmethod
-    def gemm_slab_bytes(m: int, n: int, k: int, x_f16: bool = False, workspace: int = 32 << 20) -> int:
-        """Slab size for the library route of ``gguf_gemm_slab``: W and (unless
-        X is f16) X as f16, each rounded up to 256 bytes, plus the workspace."""
-        r = lambda v: (v + 255) // 256 * 256
+    def nf4_slab_bytes(m: int, n: int, k: int, x_f16: bool = False, workspace: int = 32 << 20) -> int:
+        """Slab size for ``nf4_gemm_slab``: W and (unless X is f16) X as
+        f16, each rounded up to 256 bytes, plus the library workspace."""
+        r = lambda v: (v + 255) // 256 * 256  # noqa: E731
         return r(2 * n * k) + (0 if x_f16 else r(2 * m * k)) + workspace
 
     def gguf_dequant(self, fmt: int, src, out, nblocks: int) -> None:

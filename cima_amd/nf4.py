@@ -252,8 +252,10 @@ class Nf4Weight:
     def gemm(self, ctx, x, y, scratch=None) -> None:
         """WTensor::gemm for a packed weight (src/quant.rs:131-162): y[m, n] = x[m, k] . W^T.
         m == 1 runs the fused GEMV; m > 1 dequantises into the ``scratch``
-        slab and multiplies with the library GEMM (cima_hip_nf4_gemm_slab);
-        ``HipCtx.gemm_slab_bytes(m, n, k)`` bytes are enough."""
+        slab a row slice at a time and multiplies each slice with the
+        library GEMM (cima_hip_nf4_gemm_slab); any slab that holds one slice
+        works (the reference's is 32 MiB), ``HipCtx.nf4_slab_bytes(m, n,
+        k)`` bytes decode W in one slice."""
         m = x.shape[0] if x.dim() == 2 else 1
         n, k = y.shape[-1], x.shape[-1]
         self._check_shape(n, k)

@@ -159,36 +159,16 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
 int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                        int m, int n, int k, int ldy, int x_dtype, int y_dtype);
 
-/* Prefill GEMM through a dequant slab: the reference's lin_gemm / WTensor::
- * gemm route (src/models/transformer.rs:618-655, src/quant.rs:120-129:
- * gguf_dequant into the DQ_SCRATCH slab, then cublasGemmEx through
- * gemm_dispatch, src/cuda.rs:2285-2320, 2468-2541), with hipBLASLt (opened
- * with dlopen) as the library.  Same arguments and result as
- * cima_hip_gguf_gemm, plus a caller-owned device slab (256-byte aligned):
- *   [W as f16, n*k*2 B][X as f16, m*k*2 B unless x_dtype is f16][workspace]
- * each part rounded up to 256 B; up to 32 MiB of the rest is the library's
- * workspace.  W is decoded bit-exactly, X rounded to f16 as the fused
- * kernel rounds it, the product accumulated in fp32.  Runs the fused kernel
- * (cima_hip_gguf_gemm) instead where that is faster (built-in rule from
- * MI355X measurements: up to 32 tokens always; 33-256 tokens unless the
- * fused grid is narrow for the row length; never past 256), when ldy != n,
- * when the slab is too small or when hipBLASLt is absent or offers no
- * algorithm; cima_hip_last_gemm_route() tells which ran.  With the
- * environment variable CIMA_GEMM_AUTOTUNE=1 at cima_hip_init, the first
- * library call of each shape times hipBLASLt's candidates (host waits).  The slab and
- * the workspace are overwritten; calls sharing a slab must be ordered. */
+/* Prefill GEMM with the engine's scratch slab: the signature of the
+ * reference's lin_gemm / WTensor::gemm route (src/models/transformer.rs:
+ * 618-655, src/quant.rs:120-129), whose gguf_dequant into the DQ_SCRATCH
+ * slab + gemm_dispatch (src/cuda.rs:2285-2320, 2468-2541) runs here as the
+ * fused MFMA kernels of cima_hip_gguf_gemm: W is dequantised tile by tile
+ * and never expanded, so the slab (256-byte aligned when given) is not
+ * touched and any size, 0 included, works.  No library GEMM is involved. */
 int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                             int m, int n, int k, int ldy, int x_dtype, int y_dtype, void* slab,
                             unsigned long long slab_bytes);
-
-/* Route threshold of cima_hip_gguf_gemm_slab (no counterpart in the
- * reference): the fewest tokens sent to the library GEMM; 0 = the
- * built-in rule. */
-int cima_hip_set_gemm_route(cima_hip_ctx* ctx, int min_tokens);
-
-/* 1 if the last cima_hip_gguf_gemm_slab call on ctx ran dequant + library
- * GEMM, 0 if it ran the fused kernel (-1 for a null context). */
-int cima_hip_last_gemm_route(cima_hip_ctx* ctx);
 
 /* Dequantise nblocks consecutive blocks to f16, bit-exact with the host
  * decoders: replaces CudaCtx::gguf_dequant (src/cuda.rs:2285-2320). */
@@ -382,12 +362,16 @@ int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, cons
 int cima_hip_set_nf4_tuning(cima_hip_ctx* ctx, int rows, int kernel);
 /* Prefill GEMM over the packed weight, Y[m, n] (row stride n) = X[m, k] .
  * W[n, k]^T: WTensor::gemm's Nf4 arm (src/quant.rs:131-162), which runs
- * nf4_dequant into the engine's slab, then gemm_f16.  Here W is decoded
- * bit-exactly (cima_hip_nf4_dequant) into the caller's 256-byte aligned
- * slab, X (f32 / bf16) rounded to f16 behind it, and hipBLASLt multiplies
- * them with fp32 accumulation; slab layout as cima_hip_gguf_gemm_slab.
- * k % 8 == 0, x 16-byte aligned.  CIMA_E_LIBRARY if hipBLASLt is absent or
- * has no algorithm for the shape. */
+ * nf4_dequant into the engine's slab, then gemm_f16.  Here X (f32 / bf16)
+ * is rounded to f16 at the head of the caller's 256-byte aligned slab, and
+ * W is decoded bit-exactly (cima_hip_nf4_dequant) into the rest a row
+ * slice at a time -- as many rows as fit beside a workspace of 1/8 of it
+ * (at most 32 MiB), slices starting on absmax block boundaries -- each
+ * slice multiplied by hipBLASLt (fp32 accumulation) into its columns of
+ * Y, as the reference works through its 32 MiB DQ_SCRATCH
+ * (src/models/transformer.rs:630-653).  k % 8 == 0, x 16-byte aligned;
+ * CIMA_E_INVALID if the slab holds no slice, CIMA_E_LIBRARY if hipBLASLt
+ * is absent or has no algorithm for the shape. */
 int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax,
                            const float* qmap, void* y, int m, int n, int k, int blocksize, int x_dtype,
                            int y_dtype, void* slab, unsigned long long slab_bytes);

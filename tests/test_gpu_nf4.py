@@ -166,7 +166,7 @@ def test_gemv_double_quantised_from_safetensors(hip, tmp_path):
     m = 5
     xs = torch.randn(m, k, device="cuda", dtype=torch.float16)
     ys = torch.empty(m, n, device="cuda", dtype=torch.float16)
-    scratch = torch.empty(hip.gemm_slab_bytes(m, n, k, x_f16=True), device="cuda", dtype=torch.uint8)
+    scratch = torch.empty(hip.nf4_slab_bytes(m, n, k, x_f16=True), device="cuda", dtype=torch.uint8)
     wt.gemm(hip, xs, ys, scratch)
     torch.cuda.synchronize()
     w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(h.packed, h.absmax, h.qmap, n * k, bs)).reshape(n, k)
@@ -239,7 +239,7 @@ def test_gemm_slab_parity(hip, m, n, k, bs):
     for xd, yd in ((2, 0), (1, 1), (0, 0)):
         x = torch.from_numpy(xf).to(TDT[xd]).cuda()
         y = torch.full((m, n), 3.0, dtype=TDT[yd], device="cuda")
-        slab = torch.empty(hip.gemm_slab_bytes(m, n, k, x_f16=xd == 1), dtype=torch.uint8, device="cuda")
+        slab = torch.empty(hip.nf4_slab_bytes(m, n, k, x_f16=xd == 1), dtype=torch.uint8, device="cuda")
         hip.nf4_gemm_slab(x, p, a, q, y, m, n, k, bs, slab)
         torch.cuda.synchronize()
         xh = x.float().cpu().numpy().astype(np.float16).astype(np.float64)
@@ -255,7 +255,7 @@ def test_gemm_slab_argument_errors(hip):
     y = torch.zeros((m, n), dtype=torch.float16, device="cuda")
     slab = torch.empty(1 << 20, dtype=torch.uint8, device="cuda")
     hip.nf4_gemm_slab(x, p, a, q, y, 0, n, k, bs, slab)  # m = 0: no-op
-    for bad in (dict(slab_bytes=2 * n * k - 1), dict(k=100)):
+    for bad in (dict(slab_bytes=256), dict(k=100)):  # 256 B: not one 256-element f16 row
         kk = bad.get("k", k)
         with pytest.raises(EngineError) as e:
             hip.nf4_gemm_slab(x, p, a, q, y, m, n, kk, bs, slab, slab_bytes=bad.get("slab_bytes"))
@@ -263,3 +263,30 @@ def test_gemm_slab_argument_errors(hip):
     with pytest.raises(EngineError) as e:
         hip.nf4_gemm_slab(x, p, a, q, y, m, n, k, bs, slab[64:])
     assert e.value.code == E_INVALID
+
+
+def test_gemm_slab_row_slices(hip):
+    """A slab far smaller than the f16 weight (the reference's 32 MiB
+    DQ_SCRATCH against a 14336 x 4096 weight's 117 MB): W is decoded and
+    multiplied a row slice at a time, each slice writing its columns of Y;
+    the result matches the one-slice run (the library may pick another
+    algorithm per slice shape, so up to summation order) and the CPU path
+    to 1e-5 on sampled rows.  A blocksize that does not divide k makes the
+    slices start on absmax block boundaries."""
+    for n, k, bs, m, slab_mb in ((14336, 4096, 64, 16, 32), (600, 192, 256, 5, 0.1)):
+        packed, absmax, qmap = case(900 + n, n * k, bs, code=RANDOM_CODE)
+        p, a, q = dev(packed), dev(absmax), dev(qmap)
+        x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        small = torch.empty(int(slab_mb * (1 << 20)), dtype=torch.uint8, device="cuda")
+        big = torch.empty(hip.nf4_slab_bytes(m, n, k), dtype=torch.uint8, device="cuda")
+        ys = torch.empty((m, n), device="cuda")
+        yb = torch.empty((m, n), device="cuda")
+        hip.nf4_gemm_slab(x, p, a, q, ys, m, n, k, bs, small)
+        hip.nf4_gemm_slab(x, p, a, q, yb, m, n, k, bs, big)
+        torch.cuda.synchronize()
+        assert rel(ys.cpu().numpy(), yb.cpu().numpy()) <= 1e-6, (n, k)
+        rows = np.random.default_rng(n).choice(n, min(n, 128), replace=False)
+        w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(packed, absmax, qmap, n * k, bs)).reshape(n, k)
+        xh = x.float().cpu().numpy().astype(np.float16).astype(np.float64)
+        want = xh @ w16[rows].astype(np.float64).T
+        assert rel(ys.cpu().numpy()[:, rows], want) <= 1e-5, (n, k)
