@@ -119,6 +119,10 @@ struct cima_hip_ctx {
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
+    // this device's copy of the decode code object's `scratch` array
+    // (cima_hip_attn_decode_noalloc), found by name at init
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
     void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
     // cached library plans: (m, n, k, y dtype, workspace cap) -> plan
     std::map<std::tuple<int, int, int, int, int, size_t>, struct LtPlan*> lt_plans;
@@ -448,6 +452,20 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         }
     }
     ctx->loaded = true;
+    {
+        // the device address of the decode module's scratch array: taken
+        // once here, with this context's device current; the array's name
+        // is not an address the host may pass to a kernel
+        hipDeviceptr_t sp = nullptr;
+        size_t sb = 0;
+        if ((e = hipModuleGetGlobal(&sp, &sb, ctx->modules[MOD_DECODE], "scratch")) != hipSuccess) {
+            unload(ctx);
+            delete ctx;
+            return fail((int)e, "hipModuleGetGlobal(scratch) failed: %s", hipGetErrorString(e));
+        }
+        ctx->scratch = (void*)sp;
+        ctx->scratch_bytes = sb;
+    }
     // resolve every kernel up front (the reference's KernelSet)
     auto add = [&](int mod, const std::string& name) -> int {
         hipFunction_t f;
@@ -1007,6 +1025,24 @@ int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_
     snprintf(name, sizeof name, "cima_attn_reduce_d%d", dim);
     void* args[] = {&part, &out, &csz, &n_chunks, &seq, &max_seq, &window, &pos_dev};
     return launch_named(ctx, name, (unsigned)q_heads, 256, args, api);
+}
+
+int cima_hip_attn_decode_noalloc(cima_hip_ctx* ctx, const void* q, const void* kc, const void* vc, void* out,
+                                 int q_heads, int kv_heads, int dim, int seq, int max_seq, int csz, int n_chunks,
+                                 float scale, int window, const int* pos_dev) {
+    const char* api = "cima_hip_attn_decode_noalloc";
+    if (int rc = ready(ctx, api)) return rc;
+    if (!ctx->scratch) return fail(CIMA_E_NOT_INIT, "%s: the decode code object has no scratch array", api);
+    if (q_heads <= 0 || dim <= 0 || n_chunks <= 0 ||
+        (unsigned long long)q_heads * (unsigned long long)n_chunks * (unsigned long long)(dim + 2) * 4ULL >
+            (unsigned long long)ctx->scratch_bytes)
+        return fail(CIMA_E_INVALID, "%s: q_heads=%d x n_chunks=%d x (dim=%d + 2) fp32 partials exceed the %zu-byte "
+                    "device scratch", api, q_heads, n_chunks, dim, ctx->scratch_bytes);
+    float* part = static_cast<float*>(ctx->scratch);
+    if (int rc = cima_hip_attn_decode_split(ctx, q, kc, vc, part, q_heads, kv_heads, dim, seq, max_seq, csz, n_chunks,
+                                            scale, window, pos_dev))
+        return rc;
+    return cima_hip_attn_reduce(ctx, part, out, q_heads, dim, csz, n_chunks, seq, max_seq, window, pos_dev);
 }
 
 int cima_hip_attn_decode(cima_hip_ctx* ctx, const void* qkv, void* kc, void* vc, float* part, int q_heads,

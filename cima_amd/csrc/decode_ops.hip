@@ -116,6 +116,12 @@ extern "C" __global__ __launch_bounds__(256) void cima_kv_append_f16(const uint1
 
 constexpr int ATT_MAX_CSZ = 256;
 
+// Device scratch of cima_hip_attn_decode_noalloc (the split partials of one
+// call, at most 4 MiB): one copy per device that loads this code object,
+// its address taken once per context with hipModuleGetGlobal.  Every call
+// on a device shares it.
+__device__ __align__(256) float scratch[(4 << 20) / 4];
+
 template <int D>
 struct AttnLds {
     float q[D];

@@ -38,7 +38,7 @@ EXPORTS = (
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
-    "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
+    "cima_hip_attn_decode_noalloc", "cima_hip_attn_decode", "cima_hip_attn_gguf_gemv", "cima_hip_gguf_gemv_argmax", "cima_hip_argmax",
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
     "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
     "cima_hip_nf4_dequant", "cima_hip_nf4_gemv", "cima_hip_set_nf4_tuning", "cima_hip_nf4_gemm_slab",
@@ -112,6 +112,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_kv_append.argtypes = [P, P, P, P, P, I, I, I, I, I, P]
     L.cima_hip_attn_decode_split.argtypes = [P, P, P, P, P, I, I, I, I, I, I, I, F, I, P]
     L.cima_hip_attn_reduce.argtypes = [P, P, P, I, I, I, I, I, I, I, P]
+    L.cima_hip_attn_decode_noalloc.argtypes = [P, P, P, P, P, I, I, I, I, I, I, I, F, I, P]
     L.cima_hip_attn_decode.argtypes = [P, P, P, P, P, I, I, I, I, I, I, F, F, I, P]
     L.cima_hip_attn_gguf_gemv.argtypes = [P, I, P, I, I, I, I, I, I, P, P, P, P, I, I]
     L.cima_hip_gguf_gemv_argmax.argtypes = [P, I, P, P, F, P, P, I, I, P]
@@ -365,6 +366,15 @@ class HipCtx:
         """CudaCtx::attn_reduce (src/cuda.rs:1476)."""
         self._check(self.lib.cima_hip_attn_reduce(self.handle, _ptr(part), _ptr(out), q_heads, dim, csz, n_chunks,
                                                   seq, max_seq, window, _ptr(pos_dev)))
+
+    def attn_decode_noalloc(self, q, kc, vc, out, q_heads: int, kv_heads: int, dim: int, seq: int, max_seq: int,
+                            csz: int, n_chunks: int, scale: float, window: int = 0, pos_dev=None) -> None:
+        """attn_decode_split + attn_reduce with the partials in the library's
+        fixed device scratch (allocates nothing; calls on one device must
+        not overlap)."""
+        self._check(self.lib.cima_hip_attn_decode_noalloc(self.handle, _ptr(q), _ptr(kc), _ptr(vc), _ptr(out),
+                                                          q_heads, kv_heads, dim, seq, max_seq, csz, n_chunks, scale,
+                                                          window, _ptr(pos_dev)))
 
     def attn_decode(self, qkv, kc, vc, part, q_heads: int, kv_heads: int, dim: int, max_seq: int, csz: int,
                     n_chunks: int, theta: float, scale: float, pos_dev, window: int = 0) -> None:

@@ -215,6 +215,18 @@ int cima_hip_attn_decode_split(cima_hip_ctx* ctx, const void* q, const void* k_c
  * CudaCtx::attn_reduce (src/cuda.rs:1476-1505). */
 int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_heads, int dim, int csz,
                          int n_chunks, int seq, int max_seq, int window, const int* pos_dev);
+/* Split decode attention and its merge in one call that allocates
+ * nothing: cima_hip_attn_decode_split + cima_hip_attn_reduce (same
+ * arguments and results), their partials kept in a fixed 4 MiB device
+ * array of the decode code object instead of a caller's workspace.  No
+ * counterpart in the reference: for callers that cannot allocate (HIP
+ * graph capture, tight serving loops, harnesses that forbid it).  Limit:
+ * q_heads * n_chunks * (dim + 2) * 4 bytes <= 4 MiB, else CIMA_E_INVALID.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one device (other streams, other contexts) race. */
+int cima_hip_attn_decode_noalloc(cima_hip_ctx* ctx, const void* q, const void* k_cache, const void* v_cache,
+                                 void* out, int q_heads, int kv_heads, int dim, int seq, int max_seq, int csz,
+                                 int n_chunks, float scale, int window, const int* pos_dev);
 /* One launch for a layer's decode attention partials at position
  * *pos_dev: RoPE of q and k from qkv = [q | k | v] (the fused q/k/v GEMV
  * output), append of the new k and v to the caches, and the split
