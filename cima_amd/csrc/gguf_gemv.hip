@@ -687,6 +687,10 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
                           int mode, int lpr_shift, const GemvExt& ext) {
     extern __shared__ __align__(16) uint8_t lds[];
+    // every kernel argument into SGPRs up front: one wait on the kernarg
+    // segment instead of one per first use, ahead of the first loads
+    asm volatile("" ::"s"(x), "s"(wa), "s"(wb), "s"(bias_a), "s"(bias_b), "s"(y), "s"(n), "s"(k), "s"(mode),
+                 "s"(lpr_shift), "s"(ext.norm_w), "s"(ext.pos_dev));
     constexpr int S = PAIR ? 2 * R : R;  // weight row streams per lane
     uint8_t* xq = lds;
     float* xs = reinterpret_cast<float*>(lds + 2 * k + 16 * (k >> F::PADSH));
@@ -705,9 +709,15 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     const int ngroups = gridDim.x * GNW * gpw;
     const int gid = (blockIdx.x * GNW + wave) * gpw + (lane >> lpr_shift);
     const int gid0 = (blockIdx.x * GNW + wave) * gpw;
-    const int per = gid0 < nrg ? (nrg - 1 - gid0) / ngroups + 1 : 0;
-    const int cnt = gid < nrg ? (nrg - 1 - gid) / ngroups + 1 : 0;
-    const int rg_last = cnt > 0 ? gid + (cnt - 1) * ngroups : nrg - 1;  // clamp target of loads
+    // row groups of this wave's first group (the loop count) and of this
+    // lane's group (which rows it writes): two integer divisions, computed
+    // only once the first loads are in flight (past a row group's last
+    // step a group re-loads a clamped row, which it never uses)
+    int per = 0, cnt = 0;
+    auto counts = [&]() {
+        per = gid0 < nrg ? (nrg - 1 - gid0) / ngroups + 1 : 0;
+        cnt = gid < nrg ? (nrg - 1 - gid) / ngroups + 1 : 0;
+    };
     const size_t row_bytes = (size_t)(k / F::BE) * F::BB;
 
     // this lane's units (clamped; `uok` masks the tail lanes)
@@ -811,7 +821,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             float e1[R], e2[R];
         };
         auto issue = [&](Item& dst, int q) {
-            const int g = min(gid + q * ngroups, rg_last);
+            const int g = min(gid + q * ngroups, nrg - 1);
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int row = min(g * R + (s % R), n - 1);
@@ -826,6 +836,8 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
+        __builtin_amdgcn_sched_barrier(0);
+        counts();
         stage(xb);
         typename F::Xf xr[ITERS];
 #pragma unroll
@@ -856,14 +868,14 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         static_assert(ITERS <= 2 && R == 1, "the stepped item ring serves one-row groups");
         constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
         const int T = (U + (ITERS << lpr_shift) - 1) / (ITERS << lpr_shift);
-        const int items = per * T;
+        int items = 0;  // per * T, once the counts are known
         struct Item {
             typename F::Raw w[S][ITERS];
             float e1[R], e2[R];
         };
         int ii = 0, is = 0;  // next item to load: row group, step
         auto issue = [&](Item& dst) {
-            const int g = min(gid + ii * ngroups, rg_last);
+            const int g = min(gid + ii * ngroups, nrg - 1);
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int row = min(g * R + (s % R), n - 1);
@@ -907,6 +919,9 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
         for (int d = 0; d < DEPTH; d++) issue(ring[d]);
+        __builtin_amdgcn_sched_barrier(0);
+        counts();
+        items = per * T;
         stage(xb);
         int base = 0;
         for (; base + DEPTH <= items; base += DEPTH) {
@@ -931,7 +946,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             float e1[R], e2[R];
         };
         auto issue = [&](Slot& dst, int i) {
-            const int g = min(gid + i * ngroups, rg_last);
+            const int g = min(gid + i * ngroups, nrg - 1);
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int row = min(g * R + (s % R), n - 1);
@@ -962,6 +977,8 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         XBatch<ACT, XB> xb;
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
         issue(bufA, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        counts();
         stage(xb);
         if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
         for (int i = 0; i < per; i += 2) {

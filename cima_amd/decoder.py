@@ -42,7 +42,7 @@ class DecoderConfig:
     tied: bool = True
     ggml_type: int = gguf.DType.Q8_0
     max_seq: int = 4096
-    attn_chunk: int = 256
+    attn_chunk: int = 128
     window: int = 0      # sliding-window attention (> 0: the last `window` positions), every layer
 
 
