@@ -125,7 +125,11 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
  *   the engine's activation type).  bias may be NULL.
  * Requires k % 32 == 0 (Q8_0, Q4_0) or k % 256 == 0 (Q4_K, Q6_K), x and y
  * 16-byte aligned, W 16-byte aligned for Q4_K and 2-byte aligned otherwise.
- * Unlike the reference, x is not quantised to q8_1: the dot runs in fp32. */
+ * Unlike the reference, x is not quantised to 8-bit q8_1: each workgroup
+ * stages it as 16-bit fixed point per 32-element block (x ~= s (256 hi +
+ * lo), hi and lo int8, error <= amax/65278 per element); the weight quants
+ * are dotted exactly in int32 (v_dot4_i32_i8 against the hi and lo planes)
+ * and the block sums scaled in fp32. */
 int cima_hip_gguf_gemv(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w,
                        const void* bias, void* y, int n, int k, int mode, int act_dtype);
 
@@ -151,10 +155,14 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
  * X[m, k] . dequant(W)[n, k]^T for m tokens.  Replaces the reference's
  * lin_gemm (src/models/transformer.rs:618-655): gguf_dequant of W into an
  * f16 slab (src/cuda.rs:2285) followed by gemm_f16 / gemm_strided_out
- * (src/cuda.rs:2468-2570), with no slab -- W is dequantised tile by tile
- * into LDS, bit-exact f16, and multiplied with f16 MFMA, fp32 accumulate.
- * x_dtype: CIMA_DT_F32, CIMA_DT_F16 or CIMA_DT_BF16 (converted to f16;
- * exact for 2^-14 <= |x| < 65520); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
+ * (src/cuda.rs:2468-2570), with no slab -- each workgroup dequantises its
+ * W tile, bit-exact f16, into LDS (128-token tiles) or straight into the
+ * MFMA operand registers (up to 64 tokens), and multiplies with f16 MFMA,
+ * fp32 accumulate.  x_dtype: CIMA_DT_F32, CIMA_DT_F16 or CIMA_DT_BF16,
+ * converted to f16 -- exact for 2^-14 <= |x| < 65520; beyond, values
+ * overflow to +-inf and below lose bits as f16 subnormals, with no error
+ * (the engine's activations are f16 already, saturated to +-65000 by its
+ * RMSNorm, so nothing is lost there); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
  * Requires k % 64 == 0 (and k % 256 for K-quants), x 16-byte aligned. */
 int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                        int m, int n, int k, int ldy, int x_dtype, int y_dtype);
