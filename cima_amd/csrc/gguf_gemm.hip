@@ -16,7 +16,7 @@
 // kernels: gemm_body_sk16 (16 tokens, four k-splits, weights dequantised
 // into the A operand registers, 16x16x32 MFMA), gemm_body_ra (32 or 64 tokens,
 // weights into the A operand registers, 32x32x16 MFMA) and
-// gemm_body_wide (128 tokens, weights through LDS, 32x32x16 MFMA).
+// gemm_body_pipe (128 tokens, weights through LDS, 32x32x16 MFMA).
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -274,7 +274,7 @@ struct XTile {
 // flight, 25 us with 16-row tiles; 64-row tiles of 4 waves staging the
 // weights through LDS took 23.0 us on 14336x4096).  BN = 64: gemm_body_ra,
 // 128 rows (32 per wave) x 64 k per stage, weights dequantised straight
-// into the MFMA operand registers.  BN = 128: gemm_body_wide, 128 x 64
+// into the MFMA operand registers.  BN = 128: gemm_body_pipe, 128 x 64
 // stages through LDS on a 2 x 2 wave grid.  PF stages of weights and
 // activations are in flight in registers, in the order they are consumed
 // (the memory counter retires loads in issue order).  Measured on MI355X
@@ -291,17 +291,21 @@ template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
 // of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
 // 128-row tile and tokens [wc BN/2, (wc+1) BN/2) -- so every A fragment
 // read from LDS feeds BN/64 MFMAs and every B fragment two.  Stages of 64 k;
-// GemmTile<BN>::PF stages are in flight per workgroup
-// (measured on MI355X, 14336x4096 Q4_K: 64 tokens 52.5 -> 49.0 us from 2
-// to 4 stages, 256 tokens 83 -> 69 us from 1 to 2), and two workgroups
-// share a CU.
-
-
-template <typename D, int BN, int XT, int YT>
-__device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
+// GemmTile<BN>::PF stages are in flight per workgroup, and two workgroups
+// share a CU.  Software-pipelined: within one barrier interval the MFMAs
+// of the stage in LDS run in four k-step chunks, and between them the next
+// stage is dequantised into the other LDS buffer (chunk 0: the weights,
+// chunks 1-2: the activation words, chunk 3: the weight rows written);
+// fragments are read one k-step ahead, and sched_barrier keeps each chunk's
+// instructions together so the matrix core runs under the VALU work.
+// Measured on MI355X (Q4_K, bf16 X, 512 tokens): 116 -> 107 us on
+// 14336x4096 against dequantising a stage only after the previous one's
+// MFMAs, bit-identical results.
+template <typename D, int BN, int XT, int YT, int PF>
+__device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
                                int m, int n, int k, int ldy) {
-    constexpr int BM = 128, BK = 64, KP = BK + 8, PF = GemmTile<BN>::PF;
-    constexpr int TB = BN / 64;  // 32-token MFMA tiles per wave
+    constexpr int BM = 128, BK = 64, KP = BK + 8;
+    constexpr int TB = BN / 64;
     __shared__ __align__(16) uint16_t wl[2][BM * KP];
     __shared__ __align__(16) uint16_t xl[2][BN * KP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -309,10 +313,10 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
     const int r0 = blockIdx.x * BM, t0 = blockIdx.y * BN;
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
     const int nk = k / BK;
-
     const int wrow = tid >> 1, wsub = tid & 1;
     const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
     using XS = XTile<XT, BN, BK>;
+    static_assert(XS::NL % 2 == 0, "x words split over two chunks");
     const typename XS::Map xm = XS::map(t0, m, k, KP);
     struct Stage {
         typename D::Raw wr;
@@ -323,7 +327,28 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
         st.wr = D::load(wp, 2 * sc + wsub);
         st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
     };
-
+    // activation words [i0, i1) of a raw stage -> f16 in LDS buffer buf
+    auto xstore = [&](const XS& xr, int buf, int i0, int i1) {
+#pragma unroll
+        for (int i = 0; i < XS::NL; i++) {
+            if (i < i0 || i >= i1) continue;
+            uint16_t* dst = &xl[buf][xm.lds[i]];
+            const uint32_t wv[4] = {xr.r[i].x, xr.r[i].y, xr.r[i].z, xr.r[i].w};
+            if constexpr (XT == XT_F16) {
+                *reinterpret_cast<uint4*>(dst) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
+            } else if constexpr (XT == XT_BF16) {
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    o[j] = f2h2(__builtin_bit_cast(float, wv[j] << 16), __builtin_bit_cast(float, wv[j] & 0xffff0000u));
+                *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+            } else {
+                *reinterpret_cast<uint2*>(dst) =
+                    make_uint2(f2h2(__builtin_bit_cast(float, wv[0]), __builtin_bit_cast(float, wv[1])),
+                               f2h2(__builtin_bit_cast(float, wv[2]), __builtin_bit_cast(float, wv[3])));
+            }
+        }
+    };
     float16_t acc[2][TB];
 #pragma unroll
     for (int a = 0; a < 2; a++)
@@ -331,58 +356,74 @@ __device__ void gemm_body_wide(const void* __restrict__ x, const uint8_t* __rest
         for (int b = 0; b < TB; b++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[a][b][i] = 0.f;
-
+    auto rd = [&](int buf, int ks, half8_t (&a_)[2], half8_t (&b_)[TB]) {
+        const int kof = 16 * ks + 8 * (lane >> 5);
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+            a_[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(64 * wr + 32 * a + (lane & 31)) * KP + kof]);
+#pragma unroll
+        for (int b = 0; b < TB; b++)
+            b_[b] = *reinterpret_cast<const half8_t*>(&xl[buf][((BN / 2) * wc + 32 * b + (lane & 31)) * KP + kof]);
+    };
+    auto mfma4 = [&](const half8_t (&a_)[2], const half8_t (&b_)[TB]) {
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int b = 0; b < TB; b++)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_[a], b_[b], acc[a][b], 0, 0, 0);
+    };
     Stage ring[PF];
 #pragma unroll
     for (int i = 0; i < PF; i++) issue(ring[i], i);
-
-    auto step = [&](Stage& st, int s, bool next) {
-        const int buf = s & 1;
-        {
-            uint32_t o[16];
-            D::deq(st.wr, 2 * s + wsub, o);
-            uint4* dst = reinterpret_cast<uint4*>(&wl[buf][wrow * KP + 32 * wsub]);
+    {
+        uint32_t o[16];
+        D::deq(ring[0].wr, wsub, o);
+        uint4* dst = reinterpret_cast<uint4*>(&wl[0][wrow * KP + 32 * wsub]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+        xstore(ring[0].xr, 0, 0, XS::NL);
+        issue(ring[0], PF);
+    }
+    __syncthreads();
+    // step s: multiply stage s (buffer s & 1) while stage s + 1 (ring
+    // slot nxt) is decoded into buffer (s + 1) & 1; `more`: stage s + 1
+    // exists
+    auto step = [&](Stage& nxt, int s, bool more) {
+        const int buf = s & 1, nb = buf ^ 1;
+        half8_t fa[2][2], fb[2][TB];
+        uint32_t o[16];
+        rd(buf, 0, fa[0], fb[0]);
+        rd(buf, 1, fa[1], fb[1]);
+        if (more) D::deq(nxt.wr, 2 * (s + 1) + wsub, o);
+        mfma4(fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        rd(buf, 2, fa[0], fb[0]);
+        if (more) xstore(nxt.xr, nb, 0, XS::NL / 2);
+        mfma4(fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        rd(buf, 3, fa[1], fb[1]);
+        if (more) xstore(nxt.xr, nb, XS::NL / 2, XS::NL);
+        mfma4(fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
+            uint4* dst = reinterpret_cast<uint4*>(&wl[nb][wrow * KP + 32 * wsub]);
 #pragma unroll
             for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+            issue(nxt, s + 1 + PF);
         }
-        st.xr.store(xl[buf], xm);
+        mfma4(fa[1], fb[1]);
         __syncthreads();
-        if (next) issue(st, s + PF);
-        // keep the loads ahead of the MFMAs (the scheduler would otherwise
-        // sink them below, leaving no load in flight during the multiply)
-        __builtin_amdgcn_sched_barrier(0);
-        // lane l: A[i = l%32][k = 8(l/32) + j], B[k = 8(l/32) + j][n = l%32]
-#pragma unroll
-        for (int ks = 0; ks < BK / 16; ks++) {
-            const int kof = 16 * ks + 8 * (lane >> 5);
-            half8_t av[2], bv[TB];
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-                av[a] = *reinterpret_cast<const half8_t*>(&wl[buf][(64 * wr + 32 * a + (lane & 31)) * KP + kof]);
-#pragma unroll
-            for (int b = 0; b < TB; b++)
-                bv[b] = *reinterpret_cast<const half8_t*>(&xl[buf][((BN / 2) * wc + 32 * b + (lane & 31)) * KP + kof]);
-#pragma unroll
-            for (int a = 0; a < 2; a++)
-#pragma unroll
-                for (int b = 0; b < TB; b++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[a], bv[b], acc[a][b], 0, 0, 0);
-        }
     };
-    // whole groups of PF stages with no condition in the body (a condition
-    // would make the compiler drain every load at the loop head), then the
-    // tail; stages past the end are loaded (clamped) and never consumed
     int base = 0;
-    for (; base + PF <= nk; base += PF) {
+    for (; base + PF <= nk - 1; base += PF) {
 #pragma unroll
-        for (int b0 = 0; b0 < PF; b0++) step(ring[b0], base + b0, true);
+        for (int b0 = 0; b0 < PF; b0++) step(ring[(b0 + 1) % PF], base + b0, true);
     }
 #pragma unroll
     for (int b0 = 0; b0 < PF - 1; b0++)
-        if (base + b0 < nk) step(ring[b0], base + b0, false);
+        if (base + b0 < nk - 1) step(ring[(b0 + 1) % PF], base + b0, true);
+    step(ring[0], nk - 1, false);
 
-    // lane l, element i of a 32x32 tile: row 8(i/4) + 4(l/32) + i%4, column l%32
-    // (weight row r0 + 64 wr + 32 a + row, token t0 + (BN/2) wc + 32 b + column)
 #pragma unroll
     for (int a = 0; a < 2; a++) {
 #pragma unroll
@@ -639,7 +680,7 @@ constexpr int ra_pf() {
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
         else if constexpr (BN <= 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
-        else gemm_body_wide<D, BN, XT, YT>(x, w, y, m, n, k, ldy);                                 \
+        else gemm_body_pipe<D, BN, XT, YT, GemmTile<128>::PF>(x, w, y, m, n, k, ldy);              \
     }
 #define GEMM_XY(FN, D, BN)                                                    \
     GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F32, f32)                          \
