@@ -7,8 +7,8 @@
  * device pointers (hipMalloc'd or any HIP-visible device memory), sizes are
  * element or row counts, and every call is asynchronous on the context's
  * stream.  No call allocates device memory, so all are safe inside HIP
- * graph capture once the context exists -- except the first library-routed
- * cima_hip_gguf_gemm_slab call of each shape, which creates hipBLASLt's
+ * graph capture once the context exists -- except the first
+ * cima_hip_nf4_gemm_slab call of each shape, which creates hipBLASLt's
  * handle and plan (make it once before capturing).
  *
  * Return value: 0 on success; a positive hipError_t when the HIP runtime
