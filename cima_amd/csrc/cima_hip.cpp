@@ -722,9 +722,9 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     if (bn == 16 && k % 128) bn = 32;
     // 16-token tiles: 32 rows per 512-thread workgroup, or 16 rows per
     // 256-thread workgroup (_b16n_) where 32-row tiles would leave CUs idle
-    // (measured on MI355X, Q4_K, bf16 X, m = 16: 37.3 against 41.8 us on
-    // 4096x14336, 11.1 against 12.9 on 4096x4096, 9.3 against 11.1 on
-    // 1024x4096; 25 against 18 on 14336x4096, which fills the CUs)
+    // (measured on MI355X, Q4_K, bf16 X, m = 16, with two stages in flight
+    // in the 16-row tiles: 25.8 against 41.8 us on 4096x14336, 9.2 against
+    // 12.9 on 4096x4096; 28 against 18.5 on 14336x4096, which fills the CUs)
     const bool narrow = bn == 16 && (n + 31) / 32 < ctx->num_cu;
     const int bm = narrow ? 16 : (bn == 16 ? 32 : 128);  // weight rows per workgroup
     static const char* const xn[] = {"f32", "f16", "bf16"};

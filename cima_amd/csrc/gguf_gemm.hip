@@ -690,11 +690,20 @@ constexpr int ra_pf() {
     GEMM_KERNEL(FN, D, BN, XT_F16, f16, XT_F16, f16)                          \
     GEMM_KERNEL(FN, D, BN, XT_BF16, bf16, XT_F16, f16)
 // 16-row split-k tiles (four waves) for weights too narrow to fill the CUs
-// with 32-row tiles: the _b16n_ kernels
+// with 32-row tiles: the _b16n_ kernels.  Two stages in flight at three
+// workgroups per CU where a stage's registers allow it without spilling
+// (not for f32 X, eight load words per stage, nor Q6_K), else one at four
+// (measured on MI355X, Q4_K, bf16 X, 16 tokens: 38.8 -> 25.0 us on
+// 4096x14336, 12.9 -> 9.2 on 4096x4096).
+template <typename D, int XT>
+constexpr int sk16n_pf() {
+    return (XT != XT_F32 && !std::is_same<D, DQ6_K>::value) ? 2 : 1;
+}
 #define GEMM_KERNEL_NARROW(FN, D, XT, XN, YT, YN)                                                   \
-    extern "C" __global__ __launch_bounds__(256, 4) void cima_gemm_##FN##_b16n_##XN##_##YN(         \
-        const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
-        gemm_body_sk16<D, XT, YT, 1, 1>(x, w, y, m, n, k, ldy);                                     \
+    extern "C" __global__ __launch_bounds__(256, (sk16n_pf<D, XT>() == 2 ? 3 : 4)) void            \
+    cima_gemm_##FN##_b16n_##XN##_##YN(const void* x, const uint8_t* w, void* y, int m, int n, int k, \
+                                      int ldy) {                                                    \
+        gemm_body_sk16<D, XT, YT, sk16n_pf<D, XT>(), 1>(x, w, y, m, n, k, ldy);                     \
     }
 #define GEMM_XY_NARROW(FN, D)                                                 \
     GEMM_KERNEL_NARROW(FN, D, XT_F32, f32, XT_F32, f32)                       \
