@@ -81,7 +81,7 @@ const Fmt* fmt_of(int t) {
 const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_1, CIMA_GGML_Q5_0, CIMA_GGML_Q5_1,
                         CIMA_GGML_Q4_K, CIMA_GGML_Q5_K, CIMA_GGML_Q6_K, CIMA_GGML_IQ4_XS};
 // prefill GEMM token-tile widths the code object is built for
-const int kGemmBN[] = {16, 32, 64, 128};
+const int kGemmBN[] = {16, 32, 64, 128, 256};
 
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
@@ -622,7 +622,7 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens) {
     if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemm_tile: null context");
     bool ok = tokens == 0;
     for (int b : kGemmBN) ok = ok || tokens == b;
-    if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 32, 64 or 128", tokens);
+    if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 32, 64, 128 or 256", tokens);
     ctx->tune_gemm_bn = tokens;
     return 0;
 }
@@ -709,6 +709,15 @@ int gemm_check(cima_hip_ctx* ctx, int t, const void* x, const void* w, void* y, 
 int fused_bn(int m, int n, int num_cu) {
     if (m <= 32) return 16;
     if (m <= 128) return (long long)((n + 127) / 128) * ((m + 31) / 32) <= num_cu ? 32 : 64;
+    // 256-token tiles (one workgroup per CU, the weight tile dequantised
+    // once per 256 tokens) where 128-token tiles would need more than 1.5
+    // workgroups per CU and the 256-token grid still fits one round
+    // (measured on MI355X, Q4_K, bf16 X, 14336x4096: 102.2 against 108.8 us
+    // at 512 tokens, 195 against 206 at 1024; a second round of 256-token
+    // workgroups loses: 193 against 165 at 768, and so does a grid that
+    // leaves most CUs idle: 98 against 69 on 6144x4096 at 512)
+    const long long rt = (n + 127) / 128;
+    if (rt * ((m + 255) / 256) <= num_cu && 2 * rt * ((m + 127) / 128) > 3LL * num_cu) return 256;
     return 128;
 }
 

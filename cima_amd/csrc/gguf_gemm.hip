@@ -16,7 +16,7 @@
 // kernels: gemm_body_sk16 (16 tokens, four k-splits, weights dequantised
 // into the A operand registers, 16x16x32 MFMA), gemm_body_ra (32 or 64 tokens,
 // weights into the A operand registers, 32x32x16 MFMA) and
-// gemm_body_pipe (128 tokens, weights through LDS, 32x32x16 MFMA).
+// gemm_body_pipe (128 or 256 tokens, weights through LDS, 32x32x16 MFMA).
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -286,6 +286,9 @@ template <int BN> struct GemmTile;
 template <> struct GemmTile<32> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<64> { static constexpr int BM = 128, PF = 4; };
 template <> struct GemmTile<128> { static constexpr int BM = 128, PF = 2; };
+// BN = 256: the same pipelined body with 128 tokens per wave (a 64 x 128
+// wave tile), 110 KB of LDS, one workgroup per CU.
+template <> struct GemmTile<256> { static constexpr int BM = 128, PF = 2; };
 
 // Wide token tiles (BN = 128): v_mfma_f32_32x32x16_f16 on a 2 x 2 grid
 // of waves -- wave (wr, wc) owns weight rows [64 wr, 64 wr + 64) of the
@@ -675,7 +678,7 @@ constexpr int ra_pf() {
 
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, 2) void                          \
+    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 256 ? 1 : 2) void          \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
@@ -713,7 +716,7 @@ constexpr int sk16n_pf() {
     GEMM_KERNEL_NARROW(FN, D, XT_F16, f16, XT_F16, f16)                       \
     GEMM_KERNEL_NARROW(FN, D, XT_BF16, bf16, XT_F16, f16)
 #define GEMM_FMT(FN, D) \
-    GEMM_XY(FN, D, 16) GEMM_XY_NARROW(FN, D) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128)
+    GEMM_XY(FN, D, 16) GEMM_XY_NARROW(FN, D) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128) GEMM_XY(FN, D, 256)
 
 GEMM_FMT(q8_0, DQ8_0)
 GEMM_FMT(q4_0, DQ4_0)

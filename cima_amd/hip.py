@@ -225,7 +225,7 @@ class HipCtx:
         self._check(self.lib.cima_hip_set_gemv_tuning(self.handle, rows, lanes_per_row))
 
     def set_gemm_tile(self, tokens: int = 0) -> None:
-        """Prefill GEMM token-tile width (16, 32, 64 or 128; 0 = built-in choice)."""
+        """Prefill GEMM token-tile width (16, 32, 64, 128 or 256; 0 = built-in choice)."""
         self._check(self.lib.cima_hip_set_gemm_tile(self.handle, int(tokens)))
 
     def set_gemv_grid(self, wgs_per_cu: int = 0) -> None:

@@ -107,9 +107,11 @@ int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
 int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
 /* Prefill GEMM tuning (no counterpart in the reference): token-tile width
- * (16, 32, 64 or 128) for later gguf_gemm calls; 0 = the built-in choice (16
- * up to 32 tokens; 32 up to 128 while that grid has at most one workgroup
- * per CU, else 64; 128 beyond). */
+ * (16, 32, 64, 128 or 256) for later gguf_gemm calls; 0 = the built-in
+ * choice (16 up to 32 tokens; 32 up to 128 while that grid has at most one
+ * workgroup per CU, else 64; beyond, 256 where 128-token tiles would need
+ * more than 1.5 workgroups per CU and 256-token tiles fit one per CU, else
+ * 128). */
 int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
 
 /* Fused dequant-GEMV: replaces CudaCtx::gguf_gemv (src/cuda.rs:2161-2220).

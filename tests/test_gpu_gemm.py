@@ -75,22 +75,23 @@ def test_gemm_config4_full_shape(hip, m):
 
 
 def test_gemm_tile_variants_agree(hip):
-    """Every token-tile width gives the same product (exact f16 inputs)."""
-    n, k, m = 300, 1024, 40
+    """Every token-tile width gives the same product (exact f16 inputs),
+    with one partial tile (40 tokens) and ragged ones (300 tokens)."""
+    n, k = 300, 1024
     w = synth.weights(Q4_K, 70, 0.02, n, k)
-    xf = synth.normal(71, 1.0, m * k).reshape(m, k)
     w16 = oracle.dequant(Q4_K, w, n * k)
-    x = torch.from_numpy(xf).to(torch.float16).cuda()
-    want = oracle.gemm(x.float().cpu().numpy(), w16, m, n, k)
     lib = hip.lib
-    for bn in (16, 32, 64, 128):
-        hip.handle  # noqa: B018
-        rc = lib.cima_hip_set_gemm_tile(hip.handle, bn)
-        assert rc == 0
-        y = torch.empty((m, n), device="cuda")
-        hip.gguf_gemm(Q4_K, x, torch.from_numpy(w).cuda(), y, m, n, k)
-        torch.cuda.synchronize()
-        assert rel(y.cpu().numpy(), want) <= 1e-5, bn
+    for m in (40, 300):
+        xf = synth.normal(71 + m, 1.0, m * k).reshape(m, k)
+        x = torch.from_numpy(xf).to(torch.float16).cuda()
+        want = oracle.gemm(x.float().cpu().numpy(), w16, m, n, k)
+        for bn in (16, 32, 64, 128, 256):
+            rc = lib.cima_hip_set_gemm_tile(hip.handle, bn)
+            assert rc == 0
+            y = torch.empty((m, n), device="cuda")
+            hip.gguf_gemm(Q4_K, x, torch.from_numpy(w).cuda(), y, m, n, k)
+            torch.cuda.synchronize()
+            assert rel(y.cpu().numpy(), want) <= 1e-5, (m, bn)
     lib.cima_hip_set_gemm_tile(hip.handle, 0)
 
 
@@ -112,7 +113,7 @@ def test_gemm_argument_errors(hip):
 
 
 @pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
-@pytest.mark.parametrize("bn", [16, 32, 64, 128])
+@pytest.mark.parametrize("bn", [16, 32, 64, 128, 256])
 def test_gemm_dequantises_bit_exactly(hip, t, bn):
     """With X the identity, Y = dequant(W)^T: every f16 weight the kernel
     multiplies, read back exactly (an f16 times 1.0, summed with exact
