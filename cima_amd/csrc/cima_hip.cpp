@@ -730,11 +730,13 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     if (ctx->tune_gemm_bn) bn = ctx->tune_gemm_bn;
     if (bn == 16 && k % 128) bn = 32;
     // 16-token tiles: 32 rows per 512-thread workgroup, or 16 rows per
-    // 256-thread workgroup (_b16n_) where 32-row tiles would leave CUs idle
-    // (measured on MI355X, Q4_K, bf16 X, m = 16, with two stages in flight
-    // in the 16-row tiles: 25.8 against 41.8 us on 4096x14336, 9.2 against
-    // 12.9 on 4096x4096; 28 against 18.5 on 14336x4096, which fills the CUs)
-    const bool narrow = bn == 16 && (n + 31) / 32 < ctx->num_cu;
+    // 256-thread workgroup (_b16n_) where the 32-row grid, counted over both
+    // of its dimensions, would fill at most half the CUs (measured on MI355X,
+    // Q4_K, bf16 X, 16-row against 32-row tiles, us: m = 16: 1024x4096 9.0 /
+    // 12.9, 4096x4096 9.5 / 13.2, 4096x14336 26.6 / 43.8, 6144x4096 14.8 /
+    // 13.4, 14336x4096 28.9 / 18.7; m = 24-32: 1024x4096 9.2 / 12.8,
+    // 4096x4096 14.7 / 13.5, 4096x14336 44.5 / 43.5)
+    const bool narrow = bn == 16 && 2LL * ((n + 31) / 32) * ((m + 15) / 16) <= ctx->num_cu;
     const int bm = narrow ? 16 : (bn == 16 ? 32 : 128);  // weight rows per workgroup
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];

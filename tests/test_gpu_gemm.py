@@ -139,13 +139,14 @@ def test_gemm_dequantises_bit_exactly(hip, t, bn):
 
 
 @pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
-@pytest.mark.parametrize("n", [8192, 8191, 1000])
-def test_gemm_16_token_tiles_wide_and_narrow(hip, t, n):
-    """Up to 32 tokens the weight's row count picks the split-k tile: 32 rows
-    per workgroup from 8192 rows (256 workgroups fill the CUs), 16 rows
-    (the _b16n_ kernels) below; both against the CPU path, ragged row
-    counts included."""
-    k, m = 256, 13
+@pytest.mark.parametrize("n,m", [(8192, 13), (8191, 13), (1000, 13), (4000, 32), (1000, 32), (3000, 17)])
+def test_gemm_16_token_tiles_wide_and_narrow(hip, t, n, m):
+    """Up to 32 tokens the grid picks the split-k tile: 32 rows per
+    workgroup where that grid (rows / 32 x tokens / 16) fills more than
+    half the CUs (8192 rows at 13 tokens, 4000 or 3000 rows at 17-32),
+    16 rows (the _b16n_ kernels) otherwise; both against the CPU path,
+    ragged row and token counts included."""
+    k = 256
     w = synth.weights(t, 140 + t, 0.02, n, k)
     xf = synth.normal(141, 1.0, m * k).reshape(m, k)
     w16 = oracle.dequant(t, w, n * k)
