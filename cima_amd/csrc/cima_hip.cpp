@@ -5,9 +5,8 @@
 // kernels with hipModuleLaunchKernel -- the HIP counterpart of the
 // reference's CudaCtx (src/cuda.rs), which JIT-compiles kernels.cu with
 // NVRTC and launches through cuLaunchKernel (src/cuda.rs:1112-1151).  No
-// call allocates device memory; the library route of
-// cima_hip_gguf_gemm_slab creates a hipBLASLt handle and plan on its first
-// call of a shape.
+// call allocates device memory; cima_hip_nf4_gemm_slab, the one library
+// GEMM, creates a hipBLASLt handle and plan on its first call of a shape.
 #include "cima_hip.h"
 
 #include <hip/hip_runtime.h>
@@ -123,8 +122,8 @@ struct cima_hip_ctx {
     // (cima_hip_attn_decode_noalloc), found by name at init
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
-    void* lt = nullptr;       // hipBLASLt handle, created by the first library-routed call
-    // cached library plans: (m, n, k, y dtype, workspace cap) -> plan
+    void* lt = nullptr;       // hipBLASLt handle, created by the first NF4 prefill call
+    // cached library plans: (m, n, k, ldd, y dtype, workspace cap) -> plan
     std::map<std::tuple<int, int, int, int, int, size_t>, struct LtPlan*> lt_plans;
 };
 
@@ -171,8 +170,7 @@ std::string default_code_dir() {
 
 // hipBLASLt, opened with dlopen on first use (as the reference dlopens
 // cuBLAS, src/cuda.rs:311-404): a host without it keeps every entry point
-// except the library route of cima_hip_gguf_gemm_slab, which then runs the
-// fused kernel.
+// except cima_hip_nf4_gemm_slab, which then returns CIMA_E_LIBRARY.
 struct LtApi {
     bool ok = false;
     decltype(&hipblasLtCreate) create = nullptr;
@@ -223,18 +221,11 @@ const LtApi& lt_api() {
 // one library GEMM shape: D[m, n] (row-major, ld n) = X[m, k] W[n, k]^T in
 // hipBLASLt's column-major terms D^T (n x m) = op_T(W^T as k x n) X^T (k x m)
 struct LtPlan {
-    bool ok = false;  // false: the library offers no algorithm (the fused kernel runs)
+    bool ok = false;  // false: the library offers no algorithm for the shape
     hipblasLtMatmulDesc_t desc = nullptr;
     hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-    hipblasLtMatmulAlgo_t algo;
+    hipblasLtMatmulAlgo_t algo;  // the heuristic's best-ranked one within the workspace cap
     size_t ws = 0;
-    // the heuristic's candidates (best-ranked first) and whether they have
-    // been timed on the device (autotuning)
-    static constexpr int kMaxCand = 8;
-    hipblasLtMatmulAlgo_t cand[kMaxCand];
-    size_t cand_ws[kMaxCand] = {};
-    int ncand = 0;
-    bool tuned = false;
 };
 
 namespace {
@@ -801,23 +792,22 @@ int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int ldd, int y_dtype, size_t
     if (ok) {
         hipblasLtMatmulPreference_t pref = nullptr;
         uint64_t cap = ws_cap;
-        hipblasLtMatmulHeuristicResult_t res[LtPlan::kMaxCand];
+        constexpr int kMaxCand = 8;
+        hipblasLtMatmulHeuristicResult_t res[kMaxCand];
         int found = 0;
         ok = L.pref_create(&pref) == HIPBLAS_STATUS_SUCCESS &&
              L.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof cap) == HIPBLAS_STATUS_SUCCESS &&
-             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, LtPlan::kMaxCand, res,
+             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, kMaxCand, res,
                          &found) == HIPBLAS_STATUS_SUCCESS;
         if (pref) (void)L.pref_destroy(pref);
-        for (int i = 0; ok && i < found && i < LtPlan::kMaxCand; i++)
+        bool have = false;
+        for (int i = 0; ok && !have && i < found && i < kMaxCand; i++)
             if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_cap) {
-                p->cand[p->ncand] = res[i].algo;
-                p->cand_ws[p->ncand++] = res[i].workspaceSize;
+                p->algo = res[i].algo;
+                p->ws = res[i].workspaceSize;
+                have = true;
             }
-        ok = ok && p->ncand > 0;
-        if (ok) {
-            p->algo = p->cand[0];
-            p->ws = p->cand_ws[0];
-        }
+        ok = ok && have;
     }
     p->ok = ok;
     *out = p;
@@ -835,7 +825,7 @@ int x_to_f16(cima_hip_ctx* ctx, const void* x, void* dst, long long elems, int x
     return launch(ctx, f, (unsigned)((n8 + 255) / 256), 256, args, api);
 }
 
-// Y[m, n] (ld n) = Xh[m, k] . Wh[n, k]^T through hipBLASLt, f16 operands,
+// Y[m, n] (row stride ldd) = Xh[m, k] . Wh[n, k]^T through hipBLASLt, f16 operands,
 // fp32 accumulation; *ran = false (nothing launched) when the library is
 // absent or has no algorithm for the shape within ws_cap bytes of workspace
 int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, int n, int k, int ldd, int y_dtype,

@@ -54,7 +54,7 @@ DQ_KERNELS(iq4_xs, FIQ4_XS)
 // ------------------------------------------------- activations to f16
 // Rounds n8 groups of 8 activations to f16 (round to nearest even), the
 // conversion the MFMA GEMM applies to X as it stages it in LDS: the library
-// GEMM of the dequant-slab prefill then sees the same f16 X.  f32 in:
+// GEMM of the NF4 dequant-slab prefill then sees the same f16 X.  f32 in:
 // in_bf16 = 0; bf16 in: in_bf16 = 1 (widened exactly to f32 first).
 extern "C" __global__ __launch_bounds__(256) void cima_x_to_f16(const uint4* __restrict__ src, uint4* __restrict__ dst,
                                                                 long long n8, int in_bf16) {
