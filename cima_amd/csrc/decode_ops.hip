@@ -48,12 +48,15 @@ extern "C" __global__ __launch_bounds__(256) void cima_rmsnorm_f16(const uint16_
 
 // NeoX half-split rotation of pair i (elements i and i + dim/2) at position
 // p: frequency theta^(-2i/dim) (k_rope, src/kernels.cu:397-414).
-DEV void rope_rot(float a, float b, float p, int i, int dim, float theta, float& oa, float& ob) {
-    const float freq = powf(theta, -2.0f * (float)i / (float)dim);
+DEV float rope_freq(int i, int dim, float theta) { return powf(theta, -2.0f * (float)i / (float)dim); }
+DEV void rope_rot_f(float a, float b, float p, float freq, float& oa, float& ob) {
     float s, c;
     sincosf(p * freq, &s, &c);
     oa = a * c - b * s;
     ob = a * s + b * c;
+}
+DEV void rope_rot(float a, float b, float p, int i, int dim, float theta, float& oa, float& ob) {
+    rope_rot_f(a, b, p, rope_freq(i, dim, theta), oa, ob);
 }
 
 // In place over x [rows, heads, dim]: row r sits at position pos0 + r, or
@@ -420,6 +423,13 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
             ra[j] = qkv[(size_t)(q_heads + kv_heads) * D + (size_t)kvh * D + (e - nq - D / 2)];
         }
     }
+    // the rotation frequencies do not depend on the position either
+    float fq[RI];
+#pragma unroll
+    for (int j = 0; j < RI; j++) {
+        const int e = t + NT * j;
+        fq[j] = e < nq + D / 2 ? rope_freq(e < nq ? e % (D / 2) : e - nq, D, theta) : 0.f;
+    }
     const int pos = *pos_dev;
     const int seq = min(pos + 1, max_seq);
     const int wlo = (window > 0 && seq > window) ? seq - window : 0;
@@ -437,13 +447,13 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
         if (e < nq) {
             const int h = e / (D / 2), i = e % (D / 2);
             float oa, ob;
-            rope_rot(h2f(ra[j]), h2f(rb[j]), fp, i, D, theta, oa, ob);
+            rope_rot_f(h2f(ra[j]), h2f(rb[j]), fp, fq[j], oa, ob);
             L.q[h][i] = (uint16_t)f2h(oa);
             L.q[h][i + D / 2] = (uint16_t)f2h(ob);
         } else if (has_new && e < nq + D / 2) {
             const int i = e - nq;
             float oa, ob;
-            rope_rot(h2f(ra[j]), h2f(rb[j]), fp, i, D, theta, oa, ob);
+            rope_rot_f(h2f(ra[j]), h2f(rb[j]), fp, fq[j], oa, ob);
             const uint32_t ha = f2h(oa), hb = f2h(ob);
             L.kn[i] = (uint16_t)ha;
             L.kn[i + D / 2] = (uint16_t)hb;
@@ -528,19 +538,28 @@ DEV void attn_fused_body(const uint16_t* __restrict__ qkv, uint16_t* __restrict_
     {
         const int split = NW >= TT ? wave / TT : 0;
         const int tile0 = NW >= TT ? wave % TT : wave * TPW;
+        // the range's operands read first, then four independent MFMA
+        // chains (steps st % 4) summed in a fixed order
+        constexpr int NST = PR / 4;
+        const int pb = split * PR;
+        float pv[NST], vv[TPW][NST];
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const int r = pb + 4 * st + lg;
+            pv[st] = L.p[r][lr];
+#pragma unroll
+            for (int u = 0; u < TPW; u++) vv[u][st] = h2f(L.v[r][16 * (tile0 + u) + lr]);
+        }
         at_float4 o[TPW];
 #pragma unroll
-        for (int u = 0; u < TPW; u++) o[u] = (at_float4){0.f, 0.f, 0.f, 0.f};
-        const int pb = split * PR;
-#pragma unroll 4
-        for (int st = 0; st < PR / 4; st++) {
-            const int r = pb + 4 * st + lg;
-            const float pv = L.p[r][lr];
+        for (int u = 0; u < TPW; u++) {
+            at_float4 oc[4];
 #pragma unroll
-            for (int u = 0; u < TPW; u++) {
-                const float vv = h2f(L.v[r][16 * (tile0 + u) + lr]);
-                o[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv, pv, o[u], 0, 0, 0);
-            }
+            for (int c = 0; c < 4; c++) oc[c] = (at_float4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < NST; st++)
+                oc[st & 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u][st], pv[st], oc[st & 3], 0, 0, 0);
+            o[u] = (oc[0] + oc[1]) + (oc[2] + oc[3]);
         }
         // lane l holds O[dim 16 tile + 4 lg + i][head lr]
 #pragma unroll
