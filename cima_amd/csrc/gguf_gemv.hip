@@ -566,28 +566,23 @@ struct GemvExt {
 };
 
 // Attention-merge x source: x[h*D + d] = f16(sum_c e^(m_c - M) acc_c[d] /
-// sum_c e^(m_c - M) l_c) over the live chunks c of head h, from split
-// attention partials part[(h * chunks + c) * (D + 2)] = {m, l, acc[D]} --
-// the merge of k_attn_reduce (src/kernels.cu:614-639) done by every
-// workgroup of the o-projection that consumes it, into LDS `xt` (fp32).
-// Four neighbouring lanes share a 16-element x chunk, each merging every
-// fourth partial; the four running (M, L, acc) triples then combine.
-DEV void merge_step(float& M, float& L, float a[16], float m2, float l2, const float b[16]) {
-    const float Mn = fmaxf(M, m2);
-    const float s1 = M == -INFINITY ? 0.f : __expf(M - Mn);
-    const float s2 = m2 == -INFINITY ? 0.f : __expf(m2 - Mn);
-    L = L * s1 + l2 * s2;
-#pragma unroll
-    for (int i = 0; i < 16; i++) a[i] = a[i] * s1 + b[i] * s2;
-    M = Mn;
-}
-
-// The first ATT_PRE partials of each lane (chunks sub, sub + 4, ...) are
-// loaded before the position is read -- their addresses do not depend on
-// it -- so the merge costs one memory round trip; chunks past the live
-// length or wholly before the window are skipped, never multiplied (they
-// may hold anything).
+// sum_c e^(m_c - M) l_c) over the live chunks c of head h, M = max_c m_c,
+// from split attention partials part[(h * chunks + c) * (D + 2)] = {m, l,
+// acc[D]} -- the two passes of k_attn_reduce (src/kernels.cu:614-639), done
+// by every workgroup of the o-projection that consumes it, into LDS `xt`
+// (fp32).  Four neighbouring lanes share a 16-element x chunk, each taking
+// every fourth partial: the maximum is combined across the four first, then
+// each lane's weighted sums, which are independent per chunk, and the four
+// lanes' sums add up (DPP).
+//
+// Each lane's first ATT_ML (m, l) pairs and ATT_PRE partial rows (chunks
+// sub, sub + 4, ...) are loaded before the position is read -- their
+// addresses do not depend on it -- so the merge costs one memory round trip
+// up to 4 ATT_PRE live chunks; further chunks are walked after.  Chunks
+// past the live length or wholly before the window are skipped, never
+// multiplied (they may hold anything).
 constexpr int ATT_PRE = 3;
+constexpr int ATT_ML = 8;
 
 DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, float* xt) {
     const int D = ext.att_dim, nch = ext.att_chunks, csz = ext.att_csz;
@@ -595,12 +590,14 @@ DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, f
         const int e0 = (idx >> 2) * 16, sub = idx & 3;
         const int h = e0 / D, d0 = e0 - h * D;
         const float* ph = part + (size_t)h * nch * (D + 2);
-        float2 pml[ATT_PRE];
+        float2 pml[ATT_ML];
+#pragma unroll
+        for (int j = 0; j < ATT_ML; j++)
+            pml[j] = *reinterpret_cast<const float2*>(ph + (size_t)min(sub + 4 * j, nch - 1) * (D + 2));
         float pb[ATT_PRE][16];
 #pragma unroll
         for (int j = 0; j < ATT_PRE; j++) {
             const float* pc = ph + (size_t)min(sub + 4 * j, nch - 1) * (D + 2);
-            pml[j] = *reinterpret_cast<const float2*>(pc);
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float2 v = reinterpret_cast<const float2*>(pc + 2 + d0)[i];
@@ -611,34 +608,49 @@ DEV void stage_attn(const float* __restrict__ part, int k, const GemvExt& ext, f
         const int seq = min(*ext.pos_dev + 1, ext.max_seq);
         const int wlo = (ext.att_window > 0 && seq > ext.att_window) ? seq - ext.att_window : 0;
         const int active = min((seq + csz - 1) / csz, nch), c0 = wlo / csz;
-        float M = -INFINITY, L = 0.f, a[16];
+        const int first = c0 + ((sub - c0) & 3);  // this lane's first live-range chunk
+        // pass 1: the head's maximum
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < ATT_ML; j++) {
+            const int c = sub + 4 * j;
+            if (c >= c0 && c < active) M = fmaxf(M, pml[j].x);
+        }
+        for (int c = max(sub + 4 * ATT_ML, first); c < active; c += 4) M = fmaxf(M, ph[(size_t)c * (D + 2)]);
+        M = fmaxf(M, dpp_xor1(M));
+        M = fmaxf(M, dpp_xor2(M));
+        // pass 2: the weighted sums
+        float L = 0.f, a[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) a[i] = 0.f;
 #pragma unroll
         for (int j = 0; j < ATT_PRE; j++) {
             const int c = sub + 4 * j;
-            if (c >= c0 && c < active) merge_step(M, L, a, pml[j].x, pml[j].y, pb[j]);
+            if (c >= c0 && c < active) {
+                const float w = __expf(pml[j].x - M);
+                L += w * pml[j].y;
+#pragma unroll
+                for (int i = 0; i < 16; i++) a[i] += w * pb[j][i];
+            }
         }
-        for (int c = max(sub + 4 * ATT_PRE, c0 + ((sub - c0) & 3)); c < active; c += 4) {
+        for (int c = max(sub + 4 * ATT_PRE, first); c < active; c += 4) {
             const float* pc = ph + (size_t)c * (D + 2);
             const float2 ml = *reinterpret_cast<const float2*>(pc);
-            float b[16];
+            const float w = __expf(ml.x - M);
+            L += w * ml.y;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float2 v = reinterpret_cast<const float2*>(pc + 2 + d0)[i];
-                b[2 * i] = v.x;
-                b[2 * i + 1] = v.y;
+                a[2 * i] += w * v.x;
+                a[2 * i + 1] += w * v.y;
             }
-            merge_step(M, L, a, ml.x, ml.y, b);
         }
-        {  // the four lanes of a chunk combine: lane ^ 1, then lane ^ 2 (DPP)
-            float b[16];
+        L += dpp_xor1(L);
+        L += dpp_xor2(L);
 #pragma unroll
-            for (int i = 0; i < 16; i++) b[i] = dpp_xor1(a[i]);
-            merge_step(M, L, a, dpp_xor1(M), dpp_xor1(L), b);
-#pragma unroll
-            for (int i = 0; i < 16; i++) b[i] = dpp_xor2(a[i]);
-            merge_step(M, L, a, dpp_xor2(M), dpp_xor2(L), b);
+        for (int i = 0; i < 16; i++) {
+            a[i] += dpp_xor1(a[i]);
+            a[i] += dpp_xor2(a[i]);
         }
         if (sub == 0) {
 #pragma unroll
