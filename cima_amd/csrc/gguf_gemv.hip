@@ -854,20 +854,29 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         typename F::Xf xr[ITERS];
 #pragma unroll
         for (int j = 0; j < ITERS; j++) F::loadx(xq, xs, xsum, uu[j], xr[j]);
-        for (int base = 0; base < per; base += DEPTH) {
+        auto compute = [&](const Item& it, int q) {
+            float acc[S];
+#pragma unroll
+            for (int s = 0; s < S; s++) {
+                acc[s] = 0.f;
+#pragma unroll
+                for (int j = 0; j < ITERS; j++) acc[s] += uok[j] ? wdot(it.w[s][j], xr[j], uu[j]) : 0.f;
+            }
+            finish(acc, it.e1, it.e2, q);
+        };
+        // whole rounds of DEPTH items with no condition in the body, then
+        // the wave's remaining items only (no padding item is waited for)
+        int base = 0;
+        for (; base + DEPTH <= per; base += DEPTH) {
 #pragma unroll
             for (int b = 0; b < DEPTH; b++) {
-                float acc[S];
-#pragma unroll
-                for (int s = 0; s < S; s++) {
-                    acc[s] = 0.f;
-#pragma unroll
-                    for (int j = 0; j < ITERS; j++) acc[s] += uok[j] ? wdot(ring[b].w[s][j], xr[j], uu[j]) : 0.f;
-                }
-                finish(acc, ring[b].e1, ring[b].e2, base + b);
+                compute(ring[b], base + b);
                 issue(ring[b], base + b + DEPTH);
             }
         }
+#pragma unroll
+        for (int b = 0; b < DEPTH - 1; b++)
+            if (base + b < per) compute(ring[b], base + b);
     } else if constexpr (RING == 2) {
         // Stepped item ring (long rows): a row group takes T steps of ITERS
         // units per lane, and an item is one step of one row group -- the
@@ -951,8 +960,9 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         // group; the next row group is loaded while the current one is
         // computed.  Loads are never predicated (a group's extra step
         // re-loads its own last row group, a cache hit) and issue/compute
-        // alternate unconditionally, so every loop iteration leaves exactly
-        // one row group in flight and the loop head needs no drain.
+        // alternate unconditionally within whole pairs, so every loop
+        // iteration leaves exactly one row group in flight and the loop head
+        // needs no drain; an odd count ends with one more compute.
         struct Slot {
             typename F::Raw w[S][ITERS];
             float e1[R], e2[R];
@@ -993,12 +1003,16 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         counts();
         stage(xb);
         if constexpr (ITERS == 1) F::loadx(xq, xs, xsum, uu[0], xreg);
-        for (int i = 0; i < per; i += 2) {
+        // whole pairs of row groups, then an odd wave's last one (a padding
+        // row group is loaded at most, never waited for)
+        int i = 0;
+        for (; i + 2 <= per; i += 2) {
             issue(bufB, i + 1);
             compute(bufA, i);
             issue(bufA, i + 2);
             compute(bufB, i + 1);
         }
+        if (i < per) compute(bufA, i);
     }
     if constexpr (AMAX) {
         __shared__ unsigned long long red[GNW];
