@@ -843,7 +843,11 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             }
             if constexpr (EPI) epi_load(dst.e1, dst.e2, g);
         };
-        Item ring[DEPTH];
+        // DEPTH + 1 slots: item q + DEPTH is issued into the slot freed by
+        // item q - 1 before item q is computed, so DEPTH items stay in flight
+        // while a wave computes (issuing after the compute left DEPTH - 1)
+        constexpr int NS = DEPTH + 1;
+        Item ring[NS];
         XBatch<ACT, XB> xb;
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
@@ -864,18 +868,20 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             }
             finish(acc, it.e1, it.e2, q);
         };
-        // whole rounds of DEPTH items with no condition in the body, then
-        // the wave's remaining items only (no padding item is waited for)
+        // whole rounds of NS items with no condition in the body, then the
+        // wave's remaining items (all in flight already; no padding item is
+        // waited for)
         int base = 0;
-        for (; base + DEPTH <= per; base += DEPTH) {
+        for (; base + NS <= per; base += NS) {
 #pragma unroll
-            for (int b = 0; b < DEPTH; b++) {
+            for (int b = 0; b < NS; b++) {
+                issue(ring[(b + DEPTH) % NS], base + b + DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
                 compute(ring[b], base + b);
-                issue(ring[b], base + b + DEPTH);
             }
         }
 #pragma unroll
-        for (int b = 0; b < DEPTH - 1; b++)
+        for (int b = 0; b < DEPTH; b++)
             if (base + b < per) compute(ring[b], base + b);
     } else if constexpr (RING == 2) {
         // Stepped item ring (long rows): a row group takes T steps of ITERS
@@ -935,7 +941,10 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
                 ++ci;
             }
         };
-        Item ring[DEPTH];
+        // DEPTH + 1 slots, the next item issued before the current one is
+        // consumed (as in the item ring above)
+        constexpr int NS = DEPTH + 1;
+        Item ring[NS];
         XBatch<ACT, XB> xb;
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
@@ -945,15 +954,16 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         items = per * T;
         stage(xb);
         int base = 0;
-        for (; base + DEPTH <= items; base += DEPTH) {
+        for (; base + NS <= items; base += NS) {
 #pragma unroll
-            for (int b = 0; b < DEPTH; b++) {
+            for (int b = 0; b < NS; b++) {
+                issue(ring[(b + DEPTH) % NS]);
+                __builtin_amdgcn_sched_barrier(0);
                 consume(ring[b]);
-                issue(ring[b]);
             }
         }
 #pragma unroll
-        for (int b = 0; b < DEPTH - 1; b++)
+        for (int b = 0; b < DEPTH; b++)
             if (base + b < items) consume(ring[b]);
     } else {
         // Row-group double buffer: a lane holds all ITERS units of a row
