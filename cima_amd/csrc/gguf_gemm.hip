@@ -677,8 +677,13 @@ constexpr int ra_pf() {
 }
 
 // name: cima_gemm_<fmt>_b<BN>_<x type>_<y type>
+// (HIP's second bound is the minimum waves per SIMD: the 16-token tiles
+// ask for 4, two 512-thread workgroups per CU, which the compiler then
+// schedules for -- measured on MI355X, Q4_K, bf16 X, bit-identical:
+// 14336x4096 18.4 -> 17.6 us at 16 tokens and 33.8 -> 31.0 at 32 in a
+// sweep, 18.7 -> 18.6 at 16 in bench.py's run)
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 256 ? 1 : 2) void          \
+    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 16 ? 4 : (BN == 256 ? 1 : 2)) void \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
