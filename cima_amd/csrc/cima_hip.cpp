@@ -323,7 +323,10 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     // 11.6, Q5_K 12.9 against 13.9, Q8_0 14336x8192 28.5 against 29.4).
     const bool ringl = !pair && rows == 1 && big && ctx->tune_ringl != 2 &&
                        (it == 8 || (ctx->tune_ringl == 1 && it >= 2));
-    const bool ring = !pair && rows == 1 && it <= 2 && big && !ringl;
+    // (the gate+up pair too: measured on MI355X, same process, Q4_K
+    // 2x14336x4096 14.5 -> 13.8 us cold, Q8_0 27.9 -> 27.5, against the
+    // row-group double buffer; bit-identical)
+    const bool ring = rows == 1 && it <= 2 && big && !ringl;
     return GemvPlan{rows, it, log2i(lpr), (unsigned)row_groups, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
 }
 
@@ -478,7 +481,8 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                     if (!rc) rc = add(F->gemv_module, name);
                 }
         for (int it = 1; it <= 2; it++)
-            for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax"}) {
+            for (const char* rk : {"_f32_ring", "_f32_ring_epi", "_f16_ring", "_f16_ring_epi", "_f16_ring_amax",
+                                   "_f32_ring_pair", "_f32_ring_pair_epi", "_f16_ring_pair", "_f16_ring_pair_epi"}) {
                 char name[96];
                 snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
                 if (!rc) rc = add(F->gemv_module, name);

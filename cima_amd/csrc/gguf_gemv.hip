@@ -1074,7 +1074,11 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring_epi, F, 1, IT, ACT_F32, 0, 1, 0, 0, 1)              \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring, F, 1, IT, ACT_F16, 0, 0, 0, 0, 1)                  \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 1)              \
-    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_amax, F, 1, IT, ACT_F16, 0, 0, 0, 1, 1)
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_amax, F, 1, IT, ACT_F16, 0, 0, 0, 1, 1)              \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring_pair, F, 1, IT, ACT_F32, 1, 0, 0, 0, 1)             \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring_pair_epi, F, 1, IT, ACT_F32, 1, 1, 0, 0, 1)         \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_pair, F, 1, IT, ACT_F16, 1, 0, 0, 0, 1)             \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ring_pair_epi, F, 1, IT, ACT_F16, 1, 1, 0, 0, 1)
 // stepped item-ring variants (long rows, k up to the i8 kernels'):
 // cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ringl[_epi]
 #define GEMV_RINGL_IT(FN, F, IT)                                                                       \
