@@ -301,7 +301,7 @@ def main():
                 traffic = int(float(line.split(":")[1]))
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": traffic,
-                "kernel": "cima_gemv_q4_k_r1_i1_f32_pair", "alg_bytes_per_launch": pair_bytes,
+                "kernel": "cima_gemv_q4_k_r1_i1_f32_ring_pair", "alg_bytes_per_launch": pair_bytes,
                 "avg_launch_us": round(pair_us, 3),
                 "hot_us": round(hot_us["q4_k gate+up swiglu 2x14336x4096"], 3),
                 "read_ceiling_gb_s": round(rbytes / pair_read_us / 1e3, 1),
