@@ -681,9 +681,12 @@ constexpr int ra_pf() {
 // ask for 4, two 512-thread workgroups per CU, which the compiler then
 // schedules for -- measured on MI355X, Q4_K, bf16 X, bit-identical:
 // 14336x4096 18.4 -> 17.6 us at 16 tokens and 33.8 -> 31.0 at 32 in a
-// sweep, 18.7 -> 18.6 at 16 in bench.py's run)
+// sweep, 18.7 -> 18.6 at 16 in bench.py's run; the wider tiles ask for 1,
+// which left the 64-token tile at 232 VGPRs (two workgroups per CU still
+// fit) and ran 1-3% faster than asking for 2: 14336x4096 at 48 / 64 / 128
+// tokens 35.0 -> 34.1, 35.2 -> 34.6, 44.0 -> 43.7 us)
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
-    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 16 ? 4 : (BN == 256 ? 1 : 2)) void \
+    extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 16 ? 4 : 1) void         \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
         const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
         if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
