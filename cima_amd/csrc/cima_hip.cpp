@@ -713,6 +713,12 @@ int fused_bn(int m, int n, int num_cu) {
     // leaves most CUs idle: 98 against 69 on 6144x4096 at 512)
     const long long rt = (n + 127) / 128;
     if (rt * ((m + 255) / 256) <= num_cu && 2 * rt * ((m + 127) / 128) > 3LL * num_cu) return 256;
+    // a weight too narrow for the 128-token grid to fill the CUs takes the
+    // widest register-A tile whose grid still fits one round (measured on
+    // MI355X, Q4_K, bf16 X: 4096x4096 at 256 / 512 tokens 63.0 / 63.6 us
+    // with 128-token tiles, 41.1 / 44.2 with 64-token tiles)
+    if (rt * ((m + 127) / 128) < num_cu && rt * ((m + 63) / 64) <= num_cu)
+        return rt * ((m + 31) / 32) <= num_cu ? 32 : 64;
     return 128;
 }
 

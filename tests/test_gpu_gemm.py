@@ -156,3 +156,15 @@ def test_gemm_16_token_tiles_wide_and_narrow(hip, t, n, m):
         tol = 1e-5 if xd != gguf.DT_F32 and yd == gguf.DT_F32 else 1e-3
         assert rel(y[:, :n], want) <= tol, (xd, yd)
         assert np.all(y[:, n:] == 3.0)
+
+
+@pytest.mark.parametrize("n,k,m", [(1024, 4096, 512), (4096, 4096, 256)], ids=["1024x4096_m512", "4096x4096_m256"])
+def test_gemm_narrow_weight_many_tokens(hip, n, k, m):
+    """Weights too narrow for the 128-token grid to fill the CUs run the
+    register-A tiles (32 or 64 tokens) past 128 tokens; the default route at
+    those shapes against the reference CPU path, bf16 X, fp32 Y."""
+    w = synth.weights(Q4_K, 90, 0.02, n, k)
+    xf = synth.normal(91, 1.0, m * k).reshape(m, k)
+    y, xh = run(hip, Q4_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
+    want = oracle.gemm(xh, oracle.dequant(Q4_K, w, n * k), m, n, k)
+    assert rel(y, want) <= 1e-5
