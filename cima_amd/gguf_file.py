@@ -260,7 +260,7 @@ def write(path: str, meta: Iterable[tuple], tensors: Iterable[tuple], version: i
 
 # ------------------------------------------------- the decoder in the file
 
-def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 256):
+def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128):
     """DecoderConfig from the metadata (``model_config``,
     src/formats.rs:940-1007), for the qwen2 / llama tensor family."""
     from .decoder import DecoderConfig
@@ -323,7 +323,7 @@ def _matrix(g: GGUFFile, name: str, rows: int, k: int):
     return g.tensor_data(name), int(ti.ggml_type)
 
 
-def load_model(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 256):
+def load_model(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128):
     """The qwen2 / llama-family decoder of a GGUF file as a HostModel, in
     the decode step's layout: q, k, v as one matrix when they share a
     format (else separate), gate and up as one; norms and biases as f16."""
