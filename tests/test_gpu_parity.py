@@ -393,7 +393,7 @@ def test_item_ring_matches_double_buffer(t):
     with 2) compute every row exactly as the row-group double buffer does:
     identical outputs, f32 and f16, with and without the epilogue, for rows
     of one and of two units per lane and for long rows of several steps
-    (ragged included)."""
+    (ragged included), and for the fused gate+up pair."""
     import os
     from cima_amd.hip import HipCtx
 
@@ -424,6 +424,24 @@ def test_item_ring_matches_double_buffer(t):
                 outs.append((y, y0))
             torch.cuda.synchronize()
             assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), (n, k, dt)
+    # the gate+up SwiGLU pair (each item one gate row and one up row), with
+    # and without biases
+    for n, k in ((37, 32 * ue), (1000, 32 * ue), (300, 100 * ue)):
+        wg = torch.from_numpy(synth.weights(t, 84 + n, 0.02, n, k)).cuda()
+        wu = torch.from_numpy(synth.weights(t, 85 + n, 0.02, n, k)).cuda()
+        for dt in (torch.float32, torch.float16):
+            x = torch.from_numpy(synth.normal(86, 1.0, k)).to(dt).cuda()
+            bg = torch.from_numpy(synth.normal(87, 0.1, n)).to(dt).cuda()
+            bu = torch.from_numpy(synth.normal(88, 0.1, n)).to(dt).cuda()
+            outs = []
+            for mode, c in ctxs.items():
+                y = torch.empty(n, dtype=dt, device="cuda")
+                c.gguf_gemv_swiglu(t, x, wg, wu, bg, bu, y, n, k)
+                y0 = torch.empty(n, dtype=dt, device="cuda")
+                c.gguf_gemv_swiglu(t, x, wg, wu, None, None, y0, n, k)
+                outs.append((y, y0))
+            torch.cuda.synchronize()
+            assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1]), ("pair", n, k, dt)
     for c in ctxs.values():
         c.close()
 
