@@ -822,9 +822,9 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 
     if constexpr (RING == 1) {
         // Item ring (single-row rows of one or two units per lane): item q
-        // is the lane's q-th row group; DEPTH items are in flight in a ring
-        // of slots and the loop body is unrolled over DEPTH items so slot
-        // indices are compile-time constants.  Items past the lane's last
+        // is the lane's q-th row group (its gate and up rows for the pair);
+        // DEPTH items are in flight in a ring of slots and the loop body is
+        // unrolled over the slots so slot indices are compile-time constants.  Items past the lane's last
         // row group re-load that row group (a cache hit) and write nothing.
         static_assert(ITERS <= 2 && R == 1, "the item ring serves one-row groups of one or two units");
         constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
@@ -1068,7 +1068,8 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_DECODE(FN, F, R, IT)
 
 // item-ring variants (one row, one or two units per lane; large matrices):
-// cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ring[_epi], cima_gemv_<fmt>_r1_i<1|2>_f16_ring_amax
+// cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ring[_pair][_epi], cima_gemv_<fmt>_r1_i<1|2>_f16_ring_amax
+// (_pair: an item is one gate row and one up row)
 #define GEMV_RING_IT(FN, F, IT)                                                                        \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring, F, 1, IT, ACT_F32, 0, 0, 0, 0, 1)                  \
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ring_epi, F, 1, IT, ACT_F32, 0, 1, 0, 0, 1)              \
