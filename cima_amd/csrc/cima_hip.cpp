@@ -5,12 +5,11 @@
 // kernels with hipModuleLaunchKernel -- the HIP counterpart of the
 // reference's CudaCtx (src/cuda.rs), which JIT-compiles kernels.cu with
 // NVRTC and launches through cuLaunchKernel (src/cuda.rs:1112-1151).  No
-// call allocates device memory; cima_hip_nf4_gemm_slab, the one library
-// GEMM, creates a hipBLASLt handle and plan on its first call of a shape.
+// call allocates device memory, and no library kernel runs: every GEMV and
+// GEMM, the bitsandbytes prefill included, is this project's own.
 #include "cima_hip.h"
 
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <dlfcn.h>
 #include <stdarg.h>
@@ -82,6 +81,9 @@ const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_1, CIMA_GGM
 // prefill GEMM token-tile widths the code object is built for
 const int kGemmBN[] = {16, 32, 64, 128, 256};
 
+// (lanes per row, unit steps) of the direct-to-LDS streaming GEMVs built
+const int kDmaShapes[][2] = {{64, 1}, {64, 2}, {32, 1}, {16, 1}};
+
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
 
@@ -116,15 +118,13 @@ struct cima_hip_ctx {
     int tune_gemm_bn = 0;  // prefill GEMM token tile (0 = smallest built one covering m)
     int tune_ring = 0;     // GEMV main loop: 0 = heuristic, 1 = item ring where built, 2 = never
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
+    int tune_dma = 0;      // direct-to-LDS streaming GEMV: 0 = heuristic, 1 = wherever built, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
     // this device's copy of the decode code object's `scratch` array
     // (cima_hip_attn_decode_noalloc), found by name at init
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
-    void* lt = nullptr;       // hipBLASLt handle, created by the first NF4 prefill call
-    // cached library plans: (m, n, k, ldd, y dtype, workspace cap) -> plan
-    std::map<std::tuple<int, int, int, int, int, size_t>, struct LtPlan*> lt_plans;
 };
 
 namespace {
@@ -166,82 +166,6 @@ std::string default_code_dir() {
         return s == std::string::npos ? std::string(".") : p.substr(0, s);
     }
     return ".";
-}
-
-// hipBLASLt, opened with dlopen on first use (as the reference dlopens
-// cuBLAS, src/cuda.rs:311-404): a host without it keeps every entry point
-// except cima_hip_nf4_gemm_slab, which then returns CIMA_E_LIBRARY.
-struct LtApi {
-    bool ok = false;
-    decltype(&hipblasLtCreate) create = nullptr;
-    decltype(&hipblasLtDestroy) destroy = nullptr;
-    decltype(&hipblasLtMatmulDescCreate) desc_create = nullptr;
-    decltype(&hipblasLtMatmulDescDestroy) desc_destroy = nullptr;
-    decltype(&hipblasLtMatmulDescSetAttribute) desc_set = nullptr;
-    decltype(&hipblasLtMatrixLayoutCreate) layout_create = nullptr;
-    decltype(&hipblasLtMatrixLayoutDestroy) layout_destroy = nullptr;
-    decltype(&hipblasLtMatmulPreferenceCreate) pref_create = nullptr;
-    decltype(&hipblasLtMatmulPreferenceDestroy) pref_destroy = nullptr;
-    decltype(&hipblasLtMatmulPreferenceSetAttribute) pref_set = nullptr;
-    decltype(&hipblasLtMatmulAlgoGetHeuristic) heuristic = nullptr;
-    decltype(&hipblasLtMatmul) matmul = nullptr;
-};
-
-const LtApi& lt_api() {
-    static LtApi api;
-    static std::once_flag once;
-    std::call_once(once, [] {
-        void* so = dlopen("libhipblaslt.so.1", RTLD_NOW | RTLD_LOCAL);
-        if (!so) so = dlopen("libhipblaslt.so", RTLD_NOW | RTLD_LOCAL);
-        if (!so) return;
-        bool ok = true;
-        auto sym = [&](auto& f, const char* name) {
-            f = reinterpret_cast<std::remove_reference_t<decltype(f)>>(dlsym(so, name));
-            ok = ok && f;
-        };
-        sym(api.create, "hipblasLtCreate");
-        sym(api.destroy, "hipblasLtDestroy");
-        sym(api.desc_create, "hipblasLtMatmulDescCreate");
-        sym(api.desc_destroy, "hipblasLtMatmulDescDestroy");
-        sym(api.desc_set, "hipblasLtMatmulDescSetAttribute");
-        sym(api.layout_create, "hipblasLtMatrixLayoutCreate");
-        sym(api.layout_destroy, "hipblasLtMatrixLayoutDestroy");
-        sym(api.pref_create, "hipblasLtMatmulPreferenceCreate");
-        sym(api.pref_destroy, "hipblasLtMatmulPreferenceDestroy");
-        sym(api.pref_set, "hipblasLtMatmulPreferenceSetAttribute");
-        sym(api.heuristic, "hipblasLtMatmulAlgoGetHeuristic");
-        sym(api.matmul, "hipblasLtMatmul");
-        api.ok = ok;  // the library stays mapped for the life of the process
-    });
-    return api;
-}
-
-}  // namespace
-
-// one library GEMM shape: D[m, n] (row-major, ld n) = X[m, k] W[n, k]^T in
-// hipBLASLt's column-major terms D^T (n x m) = op_T(W^T as k x n) X^T (k x m)
-struct LtPlan {
-    bool ok = false;  // false: the library offers no algorithm for the shape
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
-    hipblasLtMatmulAlgo_t algo;  // the heuristic's best-ranked one within the workspace cap
-    size_t ws = 0;
-};
-
-namespace {
-
-void lt_release(cima_hip_ctx* ctx) {
-    const LtApi& L = lt_api();
-    for (auto& kv : ctx->lt_plans) {
-        LtPlan* p = kv.second;
-        if (p->desc) (void)L.desc_destroy(p->desc);
-        for (auto l : {p->a, p->b, p->d})
-            if (l) (void)L.layout_destroy(l);
-        delete p;
-    }
-    ctx->lt_plans.clear();
-    if (ctx->lt) (void)L.destroy((hipblasLtHandle_t)ctx->lt);
-    ctx->lt = nullptr;
 }
 
 void unload(cima_hip_ctx* ctx) {
@@ -330,6 +254,29 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
     return GemvPlan{rows, it, log2i(lpr), (unsigned)row_groups, (unsigned)gemv_lds_bytes(F, k), ring, ringl};
 }
 
+// Direct-to-LDS streaming GEMV (the _dma kernels, RING == 3 in
+// gguf_gemv.hip).  Built for lanes per row 64 with 1 or 2 units per lane and
+// step, and 32 or 16 with 1.  An item is a segment of lpr * iters units of
+// each of the wave's 64 / lpr rows and each weight stream; its LDS slot
+// holds, per row segment, the 16-byte lines that cover it, in whole 1 KB
+// copies.  These sizes match the kernel's SEGB / NPC / NCH / SLOT.
+struct DmaPlan {
+    int lpr, iters;
+    unsigned slot;  // LDS bytes per item
+};
+DmaPlan plan_dma(const Fmt* F, int k, bool pair) {
+    const int units = k / F->gemv_unit;
+    int lpr = pow2_ceil(units);
+    if (lpr < 16) lpr = 16;
+    if (lpr > 64) lpr = 64;
+    const int iters = (lpr == 64 && units > 64) ? 2 : 1;
+    const int segb = lpr * iters * F->gemv_unit / F->block_elems * F->block_bytes;
+    const int npc = (segb + 30) / 16;
+    const int nch = (npc + 63) / 64;
+    const unsigned slot = (unsigned)((pair ? 2 : 1) * (64 / lpr) * nch * 1024);
+    return DmaPlan{lpr, iters, slot};
+}
+
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
                 const void* ba, const void* bb, void* y, int n, int k, int mode, int act, bool pair,
                 const char* api, const void* norm_w = nullptr, float eps = 0.f, GemvKind kind = GK_PLAIN,
@@ -376,9 +323,41 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
         kind_sfx = "_amax";
         if (epi) return fail(CIMA_E_INVALID, "%s: the argmax GEMV takes no bias or residual", api);
     }
-    snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s%s", F->name, p.rows, p.iters,
-             act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : (p.ringl ? "_ringl" : ""), kind_sfx,
-             epi ? "_epi" : "");
+    // Direct-to-LDS streaming.  Measured on MI355X (cold weights, us):
+    // Q8_0 14336x4096 15.4 -> 13.3 (one item in flight per wave, three
+    // workgroups per CU), the Q8_0 gate+up pair 29.8 -> 23.4 (two items in
+    // flight); slower than the register loops for Q4_K (14336x4096 8.2 ->
+    // 9.4), for rows of several segments (4096x14336: Q8_0 17.2 -> 19.1,
+    // Q4_K 9.9 -> 12.3) and for matrices of a few MB (about 1 us more), so
+    // the heuristic takes it for large Q8_0 matrices of one-segment rows.
+    bool dma = false;
+    int depth = 1;
+    const DmaPlan dplan = plan_dma(F, k, pair);
+    const bool one_seg = k / F->gemv_unit <= dplan.lpr * dplan.iters;
+    const double wbytes_all = (pair ? 2.0 : 1.0) * (double)n * (double)(k / F->block_elems) * F->block_bytes;
+    const bool dma_auto = t == CIMA_GGML_Q8_0 && one_seg && wbytes_all >= 24e6 && kind != GK_ATT;
+    if (ctx->tune_dma != 2 && !(ctx->tune_rows > 1) && !ctx->tune_lpr && (ctx->tune_dma != 0 || dma_auto)) {
+        const DmaPlan d = dplan;
+        depth = ctx->tune_dma == 3 || (ctx->tune_dma == 0 && pair) ? 2 : 1;
+        const unsigned xb = (unsigned)((gemv_lds_bytes(F, k) + 15) & ~(size_t)15) + (kind == GK_ATT ? 4u * (unsigned)k : 0u);
+        const unsigned lds = xb + (unsigned)(kGemvThreads / 64) * depth * d.slot;
+        if ((long)lds <= ctx->max_lds) {
+            dma = true;
+            p.rows = 1;
+            p.iters = d.iters;
+            p.lpr_shift = log2i(d.lpr);
+            p.lds = lds;
+            p.grid = (unsigned)n;
+            p.ring = p.ringl = false;
+        }
+    }
+    if (dma)
+        snprintf(name, sizeof name, "cima_gemv_%s_l%d_i%d_%s_dma%d%s%s", F->name, 1 << p.lpr_shift, p.iters,
+                 act == CIMA_DT_F32 ? "f32" : "f16", depth, kind_sfx, epi ? "_epi" : "");
+    else
+        snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s%s", F->name, p.rows, p.iters,
+                 act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : (p.ringl ? "_ringl" : ""), kind_sfx,
+                 epi ? "_epi" : "");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
     int threads = kGemvThreads;
@@ -394,7 +373,8 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (resident < 1) resident = 1;
     // persistent grid: one workgroup per CU for the item ring and for Q8_0,
     // two otherwise (measured on MI355X)
-    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2);
+    const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs
+                                       : (dma ? 3 : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2));
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;
@@ -487,6 +467,16 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                 snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
                 if (!rc) rc = add(F->gemv_module, name);
             }
+        for (const auto& li : kDmaShapes)
+            for (int dd = 1; dd <= 2; dd++)
+                for (const char* dk : {"f32_dma%d", "f32_dma%d_epi", "f32_dma%d_pair", "f32_dma%d_pair_epi", "f16_dma%d",
+                                       "f16_dma%d_epi", "f16_dma%d_pair", "f16_dma%d_pair_epi", "f16_dma%d_att_epi",
+                                       "f16_dma%d_amax"}) {
+                    char sfx[48], name[96];
+                    snprintf(sfx, sizeof sfx, dk, dd);
+                    snprintf(name, sizeof name, "cima_gemv_%s_l%d_i%d_%s", F->name, li[0], li[1], sfx);
+                    if (!rc) rc = add(F->gemv_module, name);
+                }
         for (const char* rk : {"_f32_ringl", "_f32_ringl_epi", "_f16_ringl", "_f16_ringl_epi"}) {
             char name[96];
             snprintf(name, sizeof name, "cima_gemv_%s_r1_i1%s", F->name, rk);
@@ -506,8 +496,25 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_dequant_") + F->name);
         if (!rc) rc = add(MOD_DEQUANT, std::string("cima_gather_") + F->name);
     }
+    // bitsandbytes weights decoded in the GEMM tiles, f16 weights, and the
+    // plain kernel for f16 weights of k % 64 != 0
+    for (const char* wn : {"nf4", "f16w"})
+        for (int bn : kGemmBN)
+            for (const char* xt : {"f32", "f16", "bf16"})
+                for (const char* yt : {"f32", "f16"}) {
+                    char name[96];
+                    snprintf(name, sizeof name, "cima_gemm_%s_b%d_%s_%s", wn, bn, xt, yt);
+                    if (!rc) rc = add(MOD_GEMM, name);
+                    if (bn == 16) {
+                        snprintf(name, sizeof name, "cima_gemm_%s_b16n_%s_%s", wn, xt, yt);
+                        if (!rc) rc = add(MOD_GEMM, name);
+                    }
+                    if (bn == 16 && !strcmp(wn, "f16w")) {
+                        snprintf(name, sizeof name, "cima_gemm_f16w_small_%s_%s", xt, yt);
+                        if (!rc) rc = add(MOD_GEMM, name);
+                    }
+                }
     if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
-    if (!rc) rc = add(MOD_DEQUANT, "cima_x_to_f16");
     for (const char* kn : {"cima_nf4_dequant_v", "cima_nf4_dequant_e", "cima_nf4_gemv_e_f16_f16",
                            "cima_nf4_gemv_e_f32_f32"})
         if (!rc) rc = add(MOD_BNB4, kn);
@@ -537,6 +544,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_WGS")) ctx->tune_wgs = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_DMA")) ctx->tune_dma = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -554,7 +562,6 @@ int cima_hip_destroy(cima_hip_ctx* ctx) {
         (void)hipStreamSynchronize(ctx->own_stream);
         (void)hipStreamDestroy(ctx->own_stream);
     }
-    lt_release(ctx);
     unload(ctx);
     delete ctx;
     return 0;
@@ -619,6 +626,13 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens) {
     for (int b : kGemmBN) ok = ok || tokens == b;
     if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 32, 64, 128 or 256", tokens);
     ctx->tune_gemm_bn = tokens;
+    return 0;
+}
+
+int cima_hip_set_gemv_dma(cima_hip_ctx* ctx, int mode) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_dma: null context");
+    if (mode < 0 || mode > 3) return fail(CIMA_E_INVALID, "cima_hip_set_gemv_dma: mode %d is not 0, 1, 2 or 3", mode);
+    ctx->tune_dma = mode;
     return 0;
 }
 
@@ -723,8 +737,20 @@ int fused_bn(int m, int n, int num_cu) {
 }
 
 // the fused MFMA dequant-GEMM (gguf_gemm.hip) on checked arguments
-int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
-               int x_dtype, int y_dtype, const char* api) {
+// kernel-argument mirror of GemmExt in gguf_gemm.hip (same member order):
+// the bitsandbytes operands; zero for the GGUF formats
+struct GemmExt {
+    const float* absmax;
+    const float* qmap;
+    long long bsz;
+    int bs_shift;
+};
+
+// Launches cima_gemm_<fname>_b<BN>[n]_<x>_<y> over Y[m, n] (row stride ldy):
+// the token tile from fused_bn (or the tuning override), 16-token tiles
+// only for k % 128 == 0.
+int gemm_launch(cima_hip_ctx* ctx, const char* fname, const void* x, const void* w, void* y, int m, int n, int k,
+                int ldy, int x_dtype, int y_dtype, const GemmExt& gext, const char* api) {
     // the 16-token tile stages 128 k at a time (32-row weight tiles in
     // 512-thread workgroups), so it needs k % 128 == 0
     int bn = fused_bn(m, n, ctx->num_cu);
@@ -741,7 +767,7 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     const int bm = narrow ? 16 : (bn == 16 ? 32 : 128);  // weight rows per workgroup
     static const char* const xn[] = {"f32", "f16", "bf16"};
     char name[96];
-    snprintf(name, sizeof name, "cima_gemm_%s_b%d%s_%s_%s", F->name, bn, narrow ? "n" : "", xn[x_dtype],
+    snprintf(name, sizeof name, "cima_gemm_%s_b%d%s_%s_%s", fname, bn, narrow ? "n" : "", xn[x_dtype],
              y_dtype == CIMA_DT_F32 ? "f32" : "f16");
     hipFunction_t f;
     if (int rc = get_fn(ctx, name, &f)) return rc;
@@ -749,11 +775,16 @@ int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, vo
     const void* wa = w;
     void* ya = y;
     int mm = m, nn = n, kk = k, ld = ldy;
-    void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
+    GemmExt ge = gext;
+    void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld, &ge};
     const unsigned threads = bn == 16 && !narrow ? 512 : 256;
     hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, threads, 1,
                                          1, 0, ctx->stream, args, nullptr);
     return e == hipSuccess ? 0 : hip_fail(e, api);
+}
+int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
+               int x_dtype, int y_dtype, const char* api) {
+    return gemm_launch(ctx, F->name, x, w, y, m, n, k, ldy, x_dtype, y_dtype, GemmExt{}, api);
 }
 
 }  // namespace
@@ -769,89 +800,7 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int t, const void* x, const void* w, v
 
 namespace {
 
-const size_t kLtWorkspaceMax = 32u << 20;  // library GEMM workspace taken from the slab's tail
-
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-
-// builds (once per shape) the hipBLASLt descriptors and the algorithm the
-// library's heuristic ranks first for them
-int lt_plan(cima_hip_ctx* ctx, int m, int n, int k, int ldd, int y_dtype, size_t ws_cap, LtPlan** out) {
-    const LtApi& L = lt_api();
-    auto key = std::make_tuple(m, n, k, ldd, y_dtype, ws_cap);
-    auto it = ctx->lt_plans.find(key);
-    if (it != ctx->lt_plans.end()) {
-        *out = it->second;
-        return 0;
-    }
-    if (!ctx->lt) {
-        hipblasLtHandle_t h = nullptr;
-        if (L.create(&h) != HIPBLAS_STATUS_SUCCESS)
-            return fail(CIMA_E_LIBRARY, "cima_hip_nf4_gemm_slab: hipblasLtCreate failed");
-        ctx->lt = h;
-    }
-    LtPlan* p = new LtPlan();
-    ctx->lt_plans[key] = p;
-    const hipDataType yt = y_dtype == CIMA_DT_F32 ? HIP_R_32F : HIP_R_16F;
-    const int32_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-    bool ok = L.desc_create(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-              L.desc_set(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta) == HIPBLAS_STATUS_SUCCESS &&
-              L.desc_set(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb) == HIPBLAS_STATUS_SUCCESS &&
-              L.layout_create(&p->a, HIP_R_16F, (uint64_t)k, (uint64_t)n, k) == HIPBLAS_STATUS_SUCCESS &&
-              L.layout_create(&p->b, HIP_R_16F, (uint64_t)k, (uint64_t)m, k) == HIPBLAS_STATUS_SUCCESS &&
-              L.layout_create(&p->d, yt, (uint64_t)n, (uint64_t)m, ldd) == HIPBLAS_STATUS_SUCCESS;
-    if (ok) {
-        hipblasLtMatmulPreference_t pref = nullptr;
-        uint64_t cap = ws_cap;
-        constexpr int kMaxCand = 8;
-        hipblasLtMatmulHeuristicResult_t res[kMaxCand];
-        int found = 0;
-        ok = L.pref_create(&pref) == HIPBLAS_STATUS_SUCCESS &&
-             L.pref_set(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &cap, sizeof cap) == HIPBLAS_STATUS_SUCCESS &&
-             L.heuristic((hipblasLtHandle_t)ctx->lt, p->desc, p->a, p->b, p->d, p->d, pref, kMaxCand, res,
-                         &found) == HIPBLAS_STATUS_SUCCESS;
-        if (pref) (void)L.pref_destroy(pref);
-        bool have = false;
-        for (int i = 0; ok && !have && i < found && i < kMaxCand; i++)
-            if (res[i].state == HIPBLAS_STATUS_SUCCESS && res[i].workspaceSize <= ws_cap) {
-                p->algo = res[i].algo;
-                p->ws = res[i].workspaceSize;
-                have = true;
-            }
-        ok = ok && have;
-    }
-    p->ok = ok;
-    *out = p;
-    return 0;
-}
-
-// rounds X (f32 or bf16, m*k elements, m*k % 8 == 0) to f16 at dst
-int x_to_f16(cima_hip_ctx* ctx, const void* x, void* dst, long long elems, int x_dtype, const char* api) {
-    hipFunction_t f;
-    if (int rc = get_fn(ctx, "cima_x_to_f16", &f)) return rc;
-    const void* src = x;
-    long long n8 = elems / 8;
-    int in_bf16 = x_dtype == CIMA_DT_BF16;
-    void* args[] = {&src, &dst, &n8, &in_bf16};
-    return launch(ctx, f, (unsigned)((n8 + 255) / 256), 256, args, api);
-}
-
-// Y[m, n] (row stride ldd) = Xh[m, k] . Wh[n, k]^T through hipBLASLt, f16 operands,
-// fp32 accumulation; *ran = false (nothing launched) when the library is
-// absent or has no algorithm for the shape within ws_cap bytes of workspace
-int lt_gemm(cima_hip_ctx* ctx, const void* wh, const void* xh, void* y, int m, int n, int k, int ldd, int y_dtype,
-            void* ws, size_t ws_cap, const char* api, bool* ran) {
-    *ran = false;
-    if (!lt_api().ok) return 0;
-    LtPlan* p = nullptr;
-    if (int rc = lt_plan(ctx, m, n, k, ldd, y_dtype, ws_cap, &p)) return rc;
-    if (!p->ok) return 0;
-    const float alpha = 1.f, beta = 0.f;
-    hipblasStatus_t st = lt_api().matmul((hipblasLtHandle_t)ctx->lt, p->desc, &alpha, wh, p->a, xh, p->b, &beta, y,
-                                         p->d, y, p->d, &p->algo, p->ws ? ws : nullptr, p->ws, ctx->stream);
-    if (st != HIPBLAS_STATUS_SUCCESS) return fail(CIMA_E_LIBRARY, "%s: hipblasLtMatmul failed (status %d)", api, (int)st);
-    *ran = true;
-    return 0;
-}
 
 
 }  // namespace
@@ -1383,13 +1332,13 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
     if (!x || !packed || !absmax || !qmap || !y || !slab) return fail(CIMA_E_INVALID, "%s: null pointer", api);
     if (!aligned(x, 16) || !aligned(y, 4) || !aligned(slab, 256))
         return fail(CIMA_E_INVALID, "%s: misaligned x (16 B), y (4 B) or slab (256 B)", api);
-    // slab layout: [X as f16, unless it is f16][one row slice of W as f16][workspace]
-    // W is decoded and multiplied a row slice at a time (the reference's
-    // lin_gemm works through its 32 MiB DQ_SCRATCH the same way,
-    // src/models/transformer.rs:630-653), each slice's product written to
-    // its columns of Y (leading dimension n).  Slices start on absmax block
-    // boundaries: g rows is the smallest count whose elements are whole blocks.
-    const size_t xbytes = x_dtype == CIMA_DT_F16 ? 0 : align256((size_t)m * k * 2);
+    if ((long long)m * k * (x_dtype == CIMA_DT_F32 ? 4 : 2) > 0xffffffffLL)
+        return fail(CIMA_E_INVALID, "%s: X of %d x %d is 4 GiB or more", api, m, k);
+    // The slab must hold one row slice of the f16 weight, as the
+    // reference's lin_gemm needs of its scratch (both routes check it, so
+    // a caller sized for the reference behaves the same here).  A slice
+    // starts on an absmax block boundary: g rows is the smallest count whose
+    // elements are whole blocks.
     long long g = blocksize;
     {
         long long a = blocksize, b = k;
@@ -1400,35 +1349,53 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
         }
         g = blocksize / a;  // blocksize / gcd(blocksize, k)
     }
-    const size_t rest = slab_bytes > xbytes ? (size_t)slab_bytes - xbytes : 0;
-    size_t ws_cap = rest / 8 < kLtWorkspaceMax ? (rest / 8) & ~(size_t)255 : kLtWorkspaceMax;
-    long long rows = (long long)((rest - ws_cap) / (2ULL * (size_t)k)) / g * g;
+    long long rows = (long long)(slab_bytes / (2ULL * (unsigned long long)k)) / g * g;
     if (rows > n) rows = n;
     if (rows < 1)
         return fail(CIMA_E_INVALID, "%s: slab of %llu bytes holds no %lld-row slice of the f16 weight (k=%d)", api,
                     slab_bytes, g, k);
-    if (!lt_api().ok) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt (libhipblaslt.so.1) could not be opened", api);
-    uint8_t* base = static_cast<uint8_t*>(slab);
-    uint8_t* wslab = base + xbytes;
-    void* ws = wslab + align256((size_t)rows * k * 2);
-    int rc = 0;
-    const void* xh = x;
-    if (x_dtype != CIMA_DT_F16) {
-        if ((rc = x_to_f16(ctx, x, base, (long long)m * k, x_dtype, api))) return rc;
-        xh = base;
+    // Fused route: the MFMA tiles decode the packed weight themselves
+    // (cima_gemm_nf4_*), the slab is not touched.  It takes every
+    // bitsandbytes checkpoint shape: k % 64 == 0, 32-element runs sharing
+    // one absmax (blocksize % 32 == 0), 16-byte aligned packed rows.
+    if (k % 64 == 0 && blocksize % 32 == 0 && aligned(packed, 16) && aligned(absmax, 4)) {
+        const int sh = (blocksize & (blocksize - 1)) == 0 ? log2i(blocksize) : -1;
+        return gemm_launch(ctx, "nf4", x, packed, y, m, n, k, n, x_dtype, y_dtype,
+                           GemmExt{absmax, qmap, (long long)blocksize, sh}, api);
+    }
+    // Slab route for the other shapes: W is decoded into the slab a row
+    // slice at a time (the reference's lin_gemm works through its 32 MiB
+    // DQ_SCRATCH the same way, src/models/transformer.rs:630-653) and each
+    // slice is multiplied by this library's f16-weight GEMM into its
+    // columns of Y (leading dimension n): the MFMA tiles when k % 64 == 0,
+    // else a plain one-thread-per-output kernel.
+    static const char* const xn[] = {"f32", "f16", "bf16"};
+    hipFunction_t small = nullptr;
+    if (k % 64) {
+        char name[64];
+        snprintf(name, sizeof name, "cima_gemm_f16w_small_%s_%s", xn[x_dtype], y_dtype == CIMA_DT_F32 ? "f32" : "f16");
+        if (int rc = get_fn(ctx, name, &small)) return rc;
     }
     const int yes = y_dtype == CIMA_DT_F32 ? 4 : 2;
     for (long long r0 = 0; r0 < n; r0 += rows) {
         const int nr = (int)std::min(rows, (long long)n - r0);
         const long long e0 = r0 * k;
-        if ((rc = cima_hip_nf4_dequant(ctx, static_cast<const uint8_t*>(packed) + e0 / 2, absmax + e0 / blocksize,
-                                       qmap, wslab, (long long)nr * k, blocksize)))
+        if (int rc = cima_hip_nf4_dequant(ctx, static_cast<const uint8_t*>(packed) + e0 / 2, absmax + e0 / blocksize,
+                                          qmap, slab, (long long)nr * k, blocksize))
             return rc;
-        bool ran = false;
-        if ((rc = lt_gemm(ctx, wslab, xh, static_cast<uint8_t*>(y) + (size_t)r0 * yes, m, nr, k, n, y_dtype, ws,
-                          ws_cap, api, &ran)))
-            return rc;
-        if (!ran) return fail(CIMA_E_LIBRARY, "%s: hipBLASLt offers no algorithm for m=%d n=%d k=%d", api, m, nr, k);
+        void* ys = static_cast<uint8_t*>(y) + (size_t)r0 * yes;
+        if (!small) {
+            if (int rc = gemm_launch(ctx, "f16w", x, slab, ys, m, nr, k, n, x_dtype, y_dtype, GemmExt{}, api))
+                return rc;
+        } else {
+            const void* xa = x;
+            const void* wa = slab;
+            void* ya = ys;
+            int mm = m, nn = nr, kk = k, ld = n;
+            void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld};
+            const long long outs = (long long)m * nr;
+            if (int rc = launch(ctx, small, (unsigned)((outs + 255) / 256), 256, args, api)) return rc;
+        }
     }
     return 0;
 }

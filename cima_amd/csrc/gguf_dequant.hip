@@ -51,31 +51,6 @@ DQ_KERNELS(q6_k, FQ6_K)
 DQ_KERNELS(iq4_xs, FIQ4_XS)
 
 
-// ------------------------------------------------- activations to f16
-// Rounds n8 groups of 8 activations to f16 (round to nearest even), the
-// conversion the MFMA GEMM applies to X as it stages it in LDS: the library
-// GEMM of the NF4 dequant-slab prefill then sees the same f16 X.  f32 in:
-// in_bf16 = 0; bf16 in: in_bf16 = 1 (widened exactly to f32 first).
-extern "C" __global__ __launch_bounds__(256) void cima_x_to_f16(const uint4* __restrict__ src, uint4* __restrict__ dst,
-                                                                long long n8, int in_bf16) {
-    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-    if (i >= n8) return;
-    if (in_bf16) {
-        const uint4 a = src[i];
-        const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-        uint32_t o[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-            o[j] = f2h2(__builtin_bit_cast(float, w[j] << 16), __builtin_bit_cast(float, w[j] & 0xffff0000u));
-        dst[i] = make_uint4(o[0], o[1], o[2], o[3]);
-    } else {
-        const uint4 a = src[2 * i], b = src[2 * i + 1];
-        dst[i] = make_uint4(f2h2(__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, a.y)),
-                            f2h2(__builtin_bit_cast(float, a.z), __builtin_bit_cast(float, a.w)),
-                            f2h2(__builtin_bit_cast(float, b.x), __builtin_bit_cast(float, b.y)),
-                            f2h2(__builtin_bit_cast(float, b.z), __builtin_bit_cast(float, b.w)));
-    }
-}
 
 // ------------------------------------------------------ bandwidth reference
 // Streams n16 16-byte words once (grid-stride, four independent loads in

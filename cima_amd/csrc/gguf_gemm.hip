@@ -203,6 +203,109 @@ struct DQ6_K {
     }
 };
 
+// Per-call operands of formats that need more than the packed weight:
+// bitsandbytes 4-bit (absmax per `bsz` elements, the 16-entry codebook).
+// The GGUF formats ignore them.
+struct GemmExt {
+    const float* absmax;
+    const float* qmap;
+    long long bsz;   // elements per absmax entry
+    int bs_shift;    // log2(bsz) when bsz is a power of two, else -1
+};
+
+// The tile bodies call D::ctx / init / load / deq with a per-call context;
+// GG adapts the context-free GGUF decoders above.
+template <typename DQ>
+struct GG {
+    static constexpr int BE = DQ::BE, BB = DQ::BB;
+    using Raw = typename DQ::Raw;
+    struct Ctx {};
+    DEV static Ctx ctx(const uint8_t*, const GemmExt&) { return Ctx{}; }
+    DEV static void init(const Ctx&) {}
+    DEV static Raw load(const Ctx&, const uint8_t* row, int j) { return DQ::load(row, j); }
+    DEV static void deq(const Ctx&, const Raw& r, int j, uint32_t (&o)[16]) { DQ::deq(r, j, o); }
+};
+
+// bitsandbytes NF4 / FP4 (src/quant.rs:18-70): a row is k/2 packed bytes,
+// element 2i in the HIGH nibble of byte i; sub-block j of a row is 16
+// bytes, and its 32 elements share one absmax (bsz % 32 == 0, k % 32 ==
+// 0, checked on the host).  The value is f16(code[nib] * absmax): one fp32
+// product rounded once to nearest even, the decode of dequant_host
+// (src/quant.rs:401-437) and k_nf4_dequant (src/kernels.cu:320-329), so the
+// MFMA operand equals the reference's decoded f16 weight.  The codebook
+// sits in LDS (16 words in 16 banks: lanes never conflict).
+struct DNF4 {
+    static constexpr int BE = 32, BB = 16;
+    struct Raw { uint4 q; float a; };
+    struct Ctx {
+        const uint8_t* base;
+        const float* absmax;
+        const float* code;
+        long long bsz;
+        int bs_shift;
+    };
+    DEV static Ctx ctx(const uint8_t* w, const GemmExt& e) {
+        __shared__ float code[16];
+        return Ctx{w, e.absmax, code, e.bsz, e.bs_shift};
+    }
+    // every thread of the workgroup calls it before its first deq
+    DEV static void init(const Ctx& c, const float* qmap) {
+        if (threadIdx.x < 16) const_cast<float*>(c.code)[threadIdx.x] = qmap[threadIdx.x];
+        __syncthreads();
+    }
+    DEV static Raw load(const Ctx& c, const uint8_t* row, int j) {
+        Raw r;
+        r.q = *reinterpret_cast<const uint4*>(row + 16 * j);
+        const long long e = (long long)(row - c.base) * 2 + 32 * j;  // flat index of the first element
+        r.a = c.absmax[c.bs_shift >= 0 ? (e >> c.bs_shift) : (e / c.bsz)];
+        return r;
+    }
+    DEV static void deq(const Ctx& c, const Raw& r, int, uint32_t (&o)[16]) {
+        const uint32_t w[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const uint32_t byte = (w[i] >> (8 * b)) & 0xFFu;
+                o[4 * i + b] = f2h2(c.code[byte >> 4] * r.a, c.code[byte & 0xFu] * r.a);
+            }
+    }
+};
+
+// f16 weights as they stand (a row is k f16 values): the tile bodies as a
+// plain f16 GEMM, for bitsandbytes shapes the fused decoder does not take,
+// decoded into the caller's slab first
+struct DF16 {
+    static constexpr int BE = 32, BB = 64;
+    struct Raw { uint4 a[4]; };
+    struct Ctx {};
+    DEV static Ctx ctx(const uint8_t*, const GemmExt&) { return Ctx{}; }
+    DEV static void init(const Ctx&) {}
+    DEV static Raw load(const Ctx&, const uint8_t* row, int j) {
+        Raw r;
+        const uint4* p = reinterpret_cast<const uint4*>(row + 64 * j);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.a[i] = p[i];
+        return r;
+    }
+    DEV static void deq(const Ctx&, const Raw& r, int, uint32_t (&o)[16]) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[4 * i] = r.a[i].x;
+            o[4 * i + 1] = r.a[i].y;
+            o[4 * i + 2] = r.a[i].z;
+            o[4 * i + 3] = r.a[i].w;
+        }
+    }
+};
+
+// D::init with the codebook for DNF4, nothing for the others
+template <typename D>
+DEV void fmt_init(const typename D::Ctx& c, const GemmExt& e) {
+    if constexpr (std::is_same<D, DNF4>::value) D::init(c, e.qmap);
+    else D::init(c);
+}
+
 // x tile loads: BN tokens x BK k per stage, as 16-byte words (V elements);
 // LR = BK / V lanes cover one token's row, so each load instruction reads
 // whole rows, and load i of thread t takes token t / LR + i * 256 / LR at
@@ -306,7 +409,7 @@ template <> struct GemmTile<256> { static constexpr int BM = 128, PF = 2; };
 // MFMAs, bit-identical results.
 template <typename D, int BN, int XT, int YT, int PF>
 __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
-                               int m, int n, int k, int ldy) {
+                               int m, int n, int k, int ldy, const GemmExt& ext) {
     constexpr int BM = 128, BK = 64, KP = BK + 8;
     constexpr int TB = BN / 64;
     __shared__ __align__(16) uint16_t wl[2][BM * KP];
@@ -315,6 +418,8 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
     const int wr = wave >> 1, wc = wave & 1;
     const int r0 = blockIdx.x * BM, t0 = blockIdx.y * BN;
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const auto dc = D::ctx(w, ext);
+    fmt_init<D>(dc, ext);
     const int nk = k / BK;
     const int wrow = tid >> 1, wsub = tid & 1;
     const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
@@ -327,7 +432,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
     };
     auto issue = [&](Stage& st, int s) {
         const int sc = min(s, nk - 1);
-        st.wr = D::load(wp, 2 * sc + wsub);
+        st.wr = D::load(dc, wp, 2 * sc + wsub);
         st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
     };
     // activation words [i0, i1) of a raw stage -> f16 in LDS buffer buf
@@ -380,7 +485,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
     for (int i = 0; i < PF; i++) issue(ring[i], i);
     {
         uint32_t o[16];
-        D::deq(ring[0].wr, wsub, o);
+        D::deq(dc, ring[0].wr, wsub, o);
         uint4* dst = reinterpret_cast<uint4*>(&wl[0][wrow * KP + 32 * wsub]);
 #pragma unroll
         for (int i = 0; i < 4; i++) dst[i] = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
@@ -397,7 +502,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
         uint32_t o[16];
         rd(buf, 0, fa[0], fb[0]);
         rd(buf, 1, fa[1], fb[1]);
-        if (more) D::deq(nxt.wr, 2 * (s + 1) + wsub, o);
+        if (more) D::deq(dc, nxt.wr, 2 * (s + 1) + wsub, o);
         mfma4(fa[0], fb[0]);
         __builtin_amdgcn_sched_barrier(0);
         rd(buf, 2, fa[0], fb[0]);
@@ -457,7 +562,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
 // summed through LDS at the end.
 template <typename D, int XT, int YT, int PF, int RT>
 __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
-                               int m, int n, int k, int ldy) {
+                               int m, int n, int k, int ldy, const GemmExt& ext) {
     constexpr int ES = XT == XT_F32 ? 4 : 2, KP = 136;  // tile pitch in halves (pads away bank conflicts)
     constexpr int NW = 4 * RT;                           // waves: RT row tiles x 4 k-splits
     constexpr int E = 32 / RT;                           // x elements per lane and stage
@@ -467,6 +572,8 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
     const int rt = wave % RT, ks = wave / RT, g = lane >> 4;
     const int r0 = blockIdx.x * (16 * RT), t0 = blockIdx.y * 16;
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const auto dc = D::ctx(w, ext);
+    fmt_init<D>(dc, ext);
     const int nk = k / 128, cnt = (nk + 3) >> 2;  // every wave runs cnt steps (a uniform barrier count)
     const uint8_t* wp = w + (size_t)min(r0 + 16 * rt + (lane & 15), n - 1) * row_bytes;
     // this lane's share of the split's x tile: E elements of one token
@@ -478,7 +585,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
     };
     auto issue = [&](Stage& st, int i) {
         const int s = min(ks + 4 * i, nk - 1);  // past the split's last stage: re-load the last one
-        st.wr = D::load(wp, 4 * s + g);
+        st.wr = D::load(dc, wp, 4 * s + g);
 #pragma unroll
         for (int j = 0; j < XW; j++) st.xr[j] = reinterpret_cast<const uint4*>(xp + (size_t)s * 128 * ES)[j];
     };
@@ -513,7 +620,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
             }
         }
         uint32_t o[16];
-        D::deq(st.wr, 4 * min(ks + 4 * i, nk - 1) + g, o);
+        D::deq(dc, st.wr, 4 * min(ks + 4 * i, nk - 1) + g, o);
         __syncthreads();
         if (next) issue(st, i + PF);
         __builtin_amdgcn_sched_barrier(0);
@@ -568,13 +675,15 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
 // LDS; per 64-k stage a wave issues 4 (RW/32) (BN/32) v_mfma_f32_32x32x16_f16.
 template <typename D, int BN, int RW, int PF, int XT, int YT>
 __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restrict__ w, void* __restrict__ y,
-                             int m, int n, int k, int ldy) {
+                             int m, int n, int k, int ldy, const GemmExt& ext) {
     constexpr int BM = 4 * RW, BK = 64, KP = BK + 8;
     constexpr int RA = RW / 32, TB = BN / 32;
     __shared__ __align__(16) uint16_t xl[2][BN * KP];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r0 = blockIdx.x * BM + RW * wave, t0 = blockIdx.y * BN;
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
+    const auto dc = D::ctx(w, ext);
+    fmt_init<D>(dc, ext);
     const int nk = k / BK;
     const int h = lane >> 5;
 
@@ -590,7 +699,7 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
     auto issue = [&](Stage& st, int s) {
         const int sc = min(s, nk - 1);  // stages past the end re-load the last one
 #pragma unroll
-        for (int a = 0; a < RA; a++) st.wr[a] = D::load(wp[a], 2 * sc + h);
+        for (int a = 0; a < RA; a++) st.wr[a] = D::load(dc, wp[a], 2 * sc + h);
         st.xr.load(x, xm, (uint32_t)(sc * BK * XS::ES));
     };
 
@@ -611,7 +720,7 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
         st.xr.store(xl[buf], xm);
         uint32_t o[RA][16];
 #pragma unroll
-        for (int a = 0; a < RA; a++) D::deq(st.wr[a], 2 * s + h, o[a]);
+        for (int a = 0; a < RA; a++) D::deq(dc, st.wr[a], 2 * s + h, o[a]);
         __syncthreads();
         if (next) issue(st, s + PF);
         __builtin_amdgcn_sched_barrier(0);
@@ -688,10 +797,11 @@ constexpr int ra_pf() {
 #define GEMM_KERNEL(FN, D, BN, XT, XN, YT, YN)                                                       \
     extern "C" __global__ __launch_bounds__(BN == 16 ? 512 : 256, BN == 16 ? 4 : 1) void         \
     cima_gemm_##FN##_b##BN##_##XN##_##YN(                                                             \
-        const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy) {                   \
-        if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy);              \
-        else if constexpr (BN <= 64) gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy); \
-        else gemm_body_pipe<D, BN, XT, YT, GemmTile<128>::PF>(x, w, y, m, n, k, ldy);              \
+        const void* x, const uint8_t* w, void* y, int m, int n, int k, int ldy, GemmExt ext) {      \
+        if constexpr (BN == 16) gemm_body_sk16<D, XT, YT, 1, 2>(x, w, y, m, n, k, ldy, ext);         \
+        else if constexpr (BN <= 64)                                                                  \
+            gemm_body_ra<D, BN, 32, ra_pf<D, BN, XT>(), XT, YT>(x, w, y, m, n, k, ldy, ext);          \
+        else gemm_body_pipe<D, BN, XT, YT, GemmTile<128>::PF>(x, w, y, m, n, k, ldy, ext);         \
     }
 #define GEMM_XY(FN, D, BN)                                                    \
     GEMM_KERNEL(FN, D, BN, XT_F32, f32, XT_F32, f32)                          \
@@ -708,13 +818,13 @@ constexpr int ra_pf() {
 // 4096x14336, 12.9 -> 9.2 on 4096x4096).
 template <typename D, int XT>
 constexpr int sk16n_pf() {
-    return (XT != XT_F32 && !std::is_same<D, DQ6_K>::value) ? 2 : 1;
+    return (XT != XT_F32 && !std::is_same<D, GG<DQ6_K>>::value && !std::is_same<D, DF16>::value) ? 2 : 1;
 }
 #define GEMM_KERNEL_NARROW(FN, D, XT, XN, YT, YN)                                                   \
     extern "C" __global__ __launch_bounds__(256, (sk16n_pf<D, XT>() == 2 ? 3 : 4)) void            \
     cima_gemm_##FN##_b16n_##XN##_##YN(const void* x, const uint8_t* w, void* y, int m, int n, int k, \
-                                      int ldy) {                                                    \
-        gemm_body_sk16<D, XT, YT, sk16n_pf<D, XT>(), 1>(x, w, y, m, n, k, ldy);                     \
+                                      int ldy, GemmExt ext) {                                       \
+        gemm_body_sk16<D, XT, YT, sk16n_pf<D, XT>(), 1>(x, w, y, m, n, k, ldy, ext);                \
     }
 #define GEMM_XY_NARROW(FN, D)                                                 \
     GEMM_KERNEL_NARROW(FN, D, XT_F32, f32, XT_F32, f32)                       \
@@ -726,12 +836,49 @@ constexpr int sk16n_pf() {
 #define GEMM_FMT(FN, D) \
     GEMM_XY(FN, D, 16) GEMM_XY_NARROW(FN, D) GEMM_XY(FN, D, 32) GEMM_XY(FN, D, 64) GEMM_XY(FN, D, 128) GEMM_XY(FN, D, 256)
 
-GEMM_FMT(q8_0, DQ8_0)
-GEMM_FMT(q4_0, DQ4_0)
-GEMM_FMT(q4_1, DQ4_1)
-GEMM_FMT(q5_0, DQ5_01<false>)
-GEMM_FMT(q5_1, DQ5_01<true>)
-GEMM_FMT(q4_k, DQ4_K)
-GEMM_FMT(q5_k, DQ5_K)
-GEMM_FMT(q6_k, DQ6_K)
-GEMM_FMT(iq4_xs, DIQ4_XS)
+GEMM_FMT(q8_0, GG<DQ8_0>)
+GEMM_FMT(q4_0, GG<DQ4_0>)
+GEMM_FMT(q4_1, GG<DQ4_1>)
+GEMM_FMT(q5_0, GG<DQ5_01<false>>)
+GEMM_FMT(q5_1, GG<DQ5_01<true>>)
+GEMM_FMT(q4_k, GG<DQ4_K>)
+GEMM_FMT(q5_k, GG<DQ5_K>)
+GEMM_FMT(q6_k, GG<DQ6_K>)
+GEMM_FMT(iq4_xs, GG<DIQ4_XS>)
+// bitsandbytes 4-bit weights decoded in the tiles, and plain f16 weights
+GEMM_FMT(nf4, DNF4)
+GEMM_FMT(f16w, DF16)
+
+// f16 weights of any k (the slab route for k % 64 != 0): one thread per
+// output, X rounded to f16 as the tiles round it, fp32 accumulation in k
+// order.  Not a fast kernel: it serves shapes no real checkpoint has.
+template <int XT, int YT>
+__device__ void gemm_small_body(const void* __restrict__ x, const uint16_t* __restrict__ w, void* __restrict__ y,
+                                int m, int n, int k, int ldy) {
+    const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (o >= (long long)m * n) return;
+    const int tok = (int)(o / n), row = (int)(o % n);
+    const uint16_t* wr = w + (size_t)row * k;
+    float acc = 0.f;
+    for (int i = 0; i < k; i++) {
+        float xv;
+        if constexpr (XT == XT_F32) xv = h2f(f2h(static_cast<const float*>(x)[(size_t)tok * k + i]));
+        else if constexpr (XT == XT_F16) xv = h2f(static_cast<const uint16_t*>(x)[(size_t)tok * k + i]);
+        else xv = h2f(f2h(__builtin_bit_cast(float, (uint32_t)static_cast<const uint16_t*>(x)[(size_t)tok * k + i] << 16)));
+        acc = fmaf(xv, h2f(wr[i]), acc);
+    }
+    const size_t off = (size_t)tok * ldy + row;
+    if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = acc;
+    else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(acc);
+}
+#define GEMM_SMALL(XT, XN, YT, YN)                                                                      \
+    extern "C" __global__ __launch_bounds__(256) void cima_gemm_f16w_small_##XN##_##YN(                 \
+        const void* x, const uint16_t* w, void* y, int m, int n, int k, int ldy) {                      \
+        gemm_small_body<XT, YT>(x, w, y, m, n, k, ldy);                                                 \
+    }
+GEMM_SMALL(XT_F32, f32, XT_F32, f32)
+GEMM_SMALL(XT_F16, f16, XT_F32, f32)
+GEMM_SMALL(XT_BF16, bf16, XT_F32, f32)
+GEMM_SMALL(XT_F32, f32, XT_F16, f16)
+GEMM_SMALL(XT_F16, f16, XT_F16, f16)
+GEMM_SMALL(XT_BF16, bf16, XT_F16, f16)

@@ -323,6 +323,51 @@ struct IQ6_K {
     }
 };
 
+// ------------------------------------------------- direct-to-LDS copies
+//
+// dma16: every lane copies the 16 bytes at its global address g into LDS at
+// byte lds + 16 * lane (global_load_lds_dwordx4, gfx950; m0 holds the
+// wave-uniform LDS address).  Written in asm so that the compiler's wait
+// counting leaves these copies alone; their waits are explicit (wait_vm).
+DEV void dma16(const void* g, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+// wait until at most N vector memory operations of this wave are in flight
+template <int N>
+DEV void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// plain loads in asm, for the same reason: 16 bytes, 4 bytes, 2 bytes
+// (zero-extended); their registers must pass through tie16 / tie32 after
+// the wait_vm that covers them and before any use
+typedef uint32_t v4u32 __attribute__((ext_vector_type(4)));
+DEV uint4 ld16_asm(const void* p) {
+    v4u32 r;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return __builtin_bit_cast(uint4, r);
+}
+DEV uint32_t ld32_asm(const void* p) {
+    uint32_t r;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+DEV uint32_t ld16b_asm(const void* p) {
+    uint32_t r;
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(r) : "v"(p) : "memory");
+    return r;
+}
+DEV void tie16(uint4& v) {
+    v4u32 r = __builtin_bit_cast(v4u32, v);
+    asm volatile("" : "+v"(r));
+    v = __builtin_bit_cast(uint4, r);
+}
+DEV void tie32(uint32_t& v) { asm volatile("" : "+v"(v)); }
+// the 32-bit LDS address of a generic pointer into LDS (the low half of
+// its flat address: the shared aperture is 4 GiB aligned)
+DEV uint32_t lds_addr(const void* p) { return (uint32_t)(uintptr_t)p; }
+
+
 // Workgroup shape: one persistent workgroup of GNW waves per CU (a single
 // dispatch wave of workgroups across the chip; x is staged once per CU).
 #ifndef CIMA_GEMV_WAVES
@@ -405,10 +450,10 @@ struct XBatch {
     static constexpr bool G = ACT == ACT_F16 && XB <= 2;
     uint4 u[XB][U];
     uint4 g[G ? XB : 1][U];
-    DEV void load(const void* __restrict__ x, int nck, const void* __restrict__ nw = nullptr) {
+    DEV void load(const void* __restrict__ x, int nck, const void* __restrict__ nw = nullptr, int c0 = 0) {
 #pragma unroll
         for (int j = 0; j < XB; j++) {
-            const int c = min((int)threadIdx.x + GNT * j, nck - 1);
+            const int c = min(c0 + (int)threadIdx.x + GNT * j, nck - 1);
             const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(x) + (size_t)c * 16 * U);
 #pragma unroll
             for (int i = 0; i < U; i++) u[j][i] = p[i];
@@ -424,6 +469,42 @@ struct XBatch {
                 }
             }
         }
+    }
+    // The same loads issued in asm, for the direct-to-LDS loop: the
+    // compiler neither counts nor waits for them, so its own waits cannot
+    // drain the weight copies issued after them; wait_asm<N> waits for
+    // them explicitly (N = vector memory operations issued since) and hands
+    // the registers back to the compiler as defined at that point.
+    DEV void load_asm(const void* __restrict__ x, int nck, const void* __restrict__ nw) {
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+            const int c = min((int)threadIdx.x + GNT * j, nck - 1);
+            const uint8_t* p = static_cast<const uint8_t*>(x) + (size_t)c * 16 * U;
+#pragma unroll
+            for (int i = 0; i < U; i++) u[j][i] = ld16_asm(p + 16 * i);
+        }
+        if constexpr (G) {
+            if (nw) {
+#pragma unroll
+                for (int j = 0; j < XB; j++) {
+                    const int c = min((int)threadIdx.x + GNT * j, nck - 1);
+                    const uint8_t* p = static_cast<const uint8_t*>(nw) + (size_t)c * 16 * U;
+#pragma unroll
+                    for (int i = 0; i < U; i++) g[j][i] = ld16_asm(p + 16 * i);
+                }
+            }
+        }
+    }
+    template <int N>
+    DEV void wait_asm() {
+        wait_vm<N>();
+#pragma unroll
+        for (int j = 0; j < XB; j++)
+#pragma unroll
+            for (int i = 0; i < U; i++) {
+                tie16(u[j][i]);
+                if constexpr (G) tie16(g[j][i]);
+            }
     }
     // norm weights of chunk j (c = threadIdx.x + GNT j)
     DEV void get_norm(const void* __restrict__ nw, int j, int c, float v[16]) const {
@@ -547,6 +628,66 @@ DEV void stage_x(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t
             }
         }
         quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
+    }
+    __syncthreads();
+}
+
+// x -> LDS for rows of any length in batches of XB chunks per thread (the
+// direct-to-LDS loop, whose row length is not fixed at compile time).  The
+// first batch is already in flight in `xb`; a row of one batch is staged
+// by stage_x.  Longer rows load batch after batch (x is a few KB, read by
+// every workgroup, so the later batches come from L2); with norm_w the
+// first pass sums the squares and the second re-reads x.
+template <int ACT, int XB, int PADSH>
+DEV void stage_x_loop(const void* __restrict__ x, int k, XBatch<ACT, XB>& xb, uint8_t* xq, float* xs, float* xsum,
+                      const void* __restrict__ norm_w, float eps) {
+    const int nck = k >> 4;
+    constexpr int PER = GNT * XB;  // chunks per batch
+    const int nb = (nck + PER - 1) / PER;
+    if (nb == 1) {
+        stage_x<ACT, XB, PADSH>(x, k, xb, xq, xs, xsum, norm_w, eps);
+        return;
+    }
+    const int t = threadIdx.x;
+    float inv = 1.f;
+    if (norm_w) {
+        float ss = 0.f;
+        for (int b = 0; b < nb; b++) {
+            if (b > 0) xb.load(x, nck, nullptr, b * PER);
+#pragma unroll
+            for (int j = 0; j < XB; j++) {
+                float v[16];
+                xb.get(j, v);
+                float sj = 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float sv = sat16(v[i]);
+                    sj += sv * sv;
+                }
+                ss += b * PER + t + GNT * j < nck ? sj : 0.f;
+            }
+        }
+        inv = 1.0f / sqrtf(block_sum(ss) / (float)k + eps);
+    }
+    for (int b = 0; b < nb; b++) {
+        if (b > 0 || norm_w) xb.load(x, nck, nullptr, b * PER);
+#pragma unroll
+        for (int j = 0; j < XB; j++) {
+            const int c = b * PER + t + GNT * j;
+            float v[16];
+            xb.get(j, v);
+            if (norm_w) {
+                float g[16];
+                load16<ACT>(norm_w, min(c, nck - 1), g);
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float h = sat16(v[i]) * inv * g[i];
+                    if constexpr (ACT == ACT_F32) v[i] = h;
+                    else v[i] = h2f(f2h(h));
+                }
+            }
+            quant_chunk<PADSH>(v, c, c < nck, xq, xs, xsum);
+        }
     }
     __syncthreads();
 }
@@ -695,7 +836,8 @@ DEV float load_act(const void* p, int i) {
 // XS = 1: x is split-attention partials (stage_attn); AMAX = 1: the f16
 // outputs also feed a greedy argmax into *ext.slot (one u64 atomic max per
 // workgroup).
-template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI, int XS, int AMAX, int RING>
+template <typename F, int R, int ITERS, int ACT, int PAIR, int EPI, int XS, int AMAX, int RING, int LPRS = 6,
+          int DD = 1>
 __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict__ wa,
                           const uint8_t* __restrict__ wb, const void* __restrict__ bias_a,
                           const void* __restrict__ bias_b, void* __restrict__ y, int n, int k,
@@ -710,7 +852,9 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     float* xs = reinterpret_cast<float*>(lds + 2 * k + 16 * (k >> F::PADSH));
     float* xsum = xs + (k >> 5);
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index as a scalar, so row and address arithmetic that only
+    // depends on it stays on the scalar unit
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & ((1 << lpr_shift) - 1);
     const int gpw = 64 >> lpr_shift;  // groups per wave
     const int U = k / F::UE;
@@ -754,7 +898,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 
     // x chunks per thread for the longest row this variant serves (ITERS
     // units of 64 lanes; 8 for the stepped item ring): k / 16 / GNT
-    constexpr int XB = ((RING == 2 ? 8 : ITERS) * F::UE * 4 + GNT - 1) / GNT;
+    constexpr int XB = RING == 3 ? 2 : ((RING == 2 ? 8 : ITERS) * F::UE * 4 + GNT - 1) / GNT;
     // x -> LDS; the caller has the first weights in flight (and, for plain
     // x, x's first batch ahead of them in `xb`)
     auto stage = [&](XBatch<ACT, XB>& xb) {
@@ -763,7 +907,10 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             stage_attn(static_cast<const float*>(x), k, ext, xt);
             XBatch<ACT_F32, XB> xa;
             xa.load(xt, k >> 4);
-            stage_x<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
+            if constexpr (RING == 3) stage_x_loop<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
+            else stage_x<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
+        } else if constexpr (RING == 3) {
+            stage_x_loop<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
         } else {
             stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
         }
@@ -967,6 +1114,190 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #pragma unroll
         for (int b = 0; b < DEPTH; b++)
             if (base + b < items) consume(ring[b]);
+    } else if constexpr (RING == 3) {
+        // Direct-to-LDS row streaming.  An item is one segment of SEGU =
+        // LPR * ITERS consecutive units of each of the wave's GPW rows (one
+        // row per lane group), for each weight stream.  It is copied from
+        // HBM into this wave's slot of LDS with global_load_lds_dwordx4:
+        // every instruction moves 64 lanes x 16 B = 1 KB of contiguous
+        // weight bytes (the 16-byte lines that hold the segment; lanes past
+        // its end repeat its last line, which costs no HBM traffic), so the
+        // whole grid reads the weight as fully coalesced 1 KB runs and no
+        // VGPRs hold weights in flight.  Lanes then decode their units from
+        // LDS (unaligned ds_read_b128 is supported on gfx950) exactly as the
+        // register paths decode them from global memory.
+        //
+        // The copies are issued in inline asm, which the compiler's wait
+        // counting does not see: each item waits for its own copies with an
+        // explicit vmcnt of the copies issued after it (loads and stores the
+        // compiler adds only make that wait stricter).  Every compiler-
+        // visible load is therefore issued before the main loop -- x, and
+        // the epilogue operands of the wave's first 64 rows, held one row
+        // per lane -- so no wait inside the loop drains the copies.
+        //
+        // Measured on MI355X against the register item ring (Q8_0 14336 x
+        // 4096, cold): one item in flight per wave with three workgroups per
+        // CU streams the weight at 0.87 of the plain read ceiling.
+        static_assert(R == 1, "direct-to-LDS streaming serves one-row groups");
+        constexpr int LPR = 1 << LPRS, GPW = 64 / LPR;
+        constexpr int SEGU = LPR * ITERS;
+        static_assert((SEGU * F::UE) % F::BE == 0, "a segment holds whole blocks");
+        constexpr int SEGB = SEGU * F::UE / F::BE * F::BB;   // segment bytes
+        constexpr int NPC = (SEGB + 15 + 15) / 16;            // 16-B lines, any start alignment
+        constexpr int NCH = (NPC + 63) / 64;                  // copy instructions per row segment
+        constexpr int SUB = NCH * 1024;                       // LDS bytes per row segment
+        constexpr int SLOT = S * GPW * SUB;                   // LDS bytes per item
+        constexpr int NI = S * GPW * NCH;                     // copies per item
+        constexpr int D = DD;                                 // items in flight per wave
+        const int nseg = (U + SEGU - 1) / SEGU;
+        const int g = lane >> LPRS;  // this lane's group in the wave
+        // LDS: x staging (and the merge's fp32 x for XS == 1), then one
+        // region of D slots per wave
+        const unsigned xbytes = XS == 1 ? (((xstage_bytes<F::PADSH>(k) + 15) & ~15) + 4 * k)
+                                        : ((xstage_bytes<F::PADSH>(k) + 15) & ~15);
+        const unsigned wofs = xbytes + (unsigned)wave * D * SLOT;
+        const uint32_t lds_base = lds_addr(lds);
+        const uint8_t* wptr[2] = {wa, PAIR ? wb : wa};
+        // copies of item q (row group q / nseg, segment q % nseg) into slot d
+        int qi = 0, qs = 0;  // next item to issue: row group, segment
+        auto issue = [&](int d) {
+            const int rg = min(gid0 + qi * ngroups, nrg - 1);
+#pragma unroll
+            for (int st = 0; st < S; st++) {
+#pragma unroll
+                for (int gg = 0; gg < GPW; gg++) {
+                    const int row = min(rg + gg, n - 1);
+                    const size_t seg0 = (size_t)row * row_bytes + (size_t)qs * SEGB;
+                    const int len = (int)min((size_t)SEGB, row_bytes - (size_t)qs * SEGB);
+                    const uintptr_t start = (uintptr_t)(wptr[st] + seg0);
+                    const uintptr_t al = start & ~(uintptr_t)15;
+                    const int last = (int)((start - al + len - 1) >> 4);  // last line index
+#pragma unroll
+                    for (int c = 0; c < NCH; c++) {
+                        const int line = min(c * 64 + lane, last);
+                        dma16(reinterpret_cast<const void*>(al + 16 * (uintptr_t)line),
+                              lds_base + wofs + d * SLOT + (st * GPW + gg) * SUB + c * 1024);
+                    }
+                }
+            }
+            if (++qs == nseg) {
+                qs = 0;
+                ++qi;
+            }
+        };
+        // x (and the RMSNorm weights) and the epilogue operands of the
+        // wave's rows j < 64 (row group j / GPW, group j % GPW; one per lane)
+        // are loaded first, in asm, then the first items' copies; one
+        // explicit wait then covers the former only
+        XBatch<ACT, XB> xb;
+        if constexpr (XS == 0) xb.load_asm(x, k >> 4, ext.norm_w);
+        float ep1 = 0.f, ep2 = 0.f;
+        constexpr int IPB = 64 / GPW;  // row groups per epilogue block
+        auto epi_row = [&](int b) {
+            const int j = b * 64 + lane;
+            return min(gid0 + (j % GPW) + (j / GPW) * ngroups, n - 1);
+        };
+        auto epi_block = [&](int b) {
+            const int row = epi_row(b);
+            ep1 = load_act<ACT>(p1, has1 ? row : 0);
+            ep2 = load_act<ACT>(p2, has2 ? row : 0);
+        };
+        uint32_t eb1 = 0, eb2 = 0;
+        if constexpr (EPI) {
+            const int row = epi_row(0);
+            constexpr int ES = ACT == ACT_F32 ? 4 : 2;
+            const uint8_t* a1 = static_cast<const uint8_t*>(p1) + (size_t)(has1 ? row : 0) * ES;
+            const uint8_t* a2 = static_cast<const uint8_t*>(p2) + (size_t)(has2 ? row : 0) * ES;
+            if constexpr (ACT == ACT_F32) {
+                eb1 = ld32_asm(a1);
+                eb2 = ld32_asm(a2);
+            } else {
+                eb1 = ld16b_asm(a1);
+                eb2 = ld16b_asm(a2);
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < D; d++) issue(d);
+        if constexpr (XS == 0) xb.template wait_asm<D * NI>();
+        else wait_vm<D * NI>();
+        if constexpr (EPI) {
+            tie32(eb1);
+            tie32(eb2);
+            ep1 = ACT == ACT_F32 ? __builtin_bit_cast(float, eb1) : h2f(eb1);
+            ep2 = ACT == ACT_F32 ? __builtin_bit_cast(float, eb2) : h2f(eb2);
+        }
+        counts();
+        stage(xb);
+        // x fragments held in registers when a row is one segment
+        typename F::Xf xr[ITERS];
+        if (nseg == 1) {
+#pragma unroll
+            for (int j = 0; j < ITERS; j++) F::loadx(xq, xs, xsum, uu[j], xr[j]);
+        }
+        const int items = per * nseg;
+        int ci = 0, cs = 0;  // next item to compute
+        float acc[S];
+#pragma unroll
+        for (int s = 0; s < S; s++) acc[s] = 0.f;
+        auto consume = [&](int d, bool xreg_ok) {
+            const int rg = gid + ci * ngroups;
+            const int row = min(rg, n - 1);
+#pragma unroll
+            for (int st = 0; st < S; st++) {
+                const size_t seg0 = (size_t)row * row_bytes + (size_t)cs * SEGB;
+                const int shift = (int)((uintptr_t)(wptr[st] + seg0) & 15);
+                const uint8_t* sp = lds + wofs + d * SLOT + (st * GPW + g) * SUB + shift;
+#pragma unroll
+                for (int j = 0; j < ITERS; j++) {
+                    const int ul = li + j * LPR;
+                    const int u = cs * SEGU + ul;
+                    const bool ok = u < U;
+                    const typename F::Raw w = F::load(sp, ok ? ul : 0);
+                    float p;
+                    if (xreg_ok) {
+                        p = wdot(w, xr[j], uu[j]);
+                    } else {
+                        typename F::Xf xf;
+                        F::loadx(xq, xs, xsum, min(u, U - 1), xf);
+                        p = wdot(w, xf, min(u, U - 1));
+                    }
+                    acc[st] += ok ? p : 0.f;
+                }
+            }
+            if (++cs == nseg) {
+                float e1[1], e2[1];
+                if constexpr (EPI) {
+                    const int j = ci * GPW + g;
+                    if (ci > 0 && ci % IPB == 0) epi_block(ci / IPB);
+                    e1[0] = __shfl(ep1, j & 63);
+                    e2[0] = __shfl(ep2, j & 63);
+                }
+                finish(acc, e1, e2, ci);
+#pragma unroll
+                for (int s = 0; s < S; s++) acc[s] = 0.f;
+                cs = 0;
+                ++ci;
+            }
+        };
+        auto run = [&](auto xreg_tag) {
+            constexpr bool XR = decltype(xreg_tag)::value;
+            int base = 0;
+            for (; base + D <= items; base += D) {
+#pragma unroll
+                for (int d = 0; d < D; d++) {
+                    wait_vm<(D - 1) * NI>();
+                    consume(d, XR);
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    issue(d);
+                }
+            }
+            wait_vm<0>();
+#pragma unroll
+            for (int d = 0; d < D; d++)
+                if (base + d < items) consume(d, XR);
+        };
+        if (nseg == 1) run(std::true_type{});
+        else run(std::false_type{});
     } else {
         // Row-group double buffer: a lane holds all ITERS units of a row
         // group; the next row group is loaded while the current one is
@@ -1091,10 +1422,34 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ringl_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 2)
 #define GEMV_RING(FN, F) GEMV_RING_IT(FN, F, 1) GEMV_RING_IT(FN, F, 2) GEMV_RINGL_IT(FN, F, 1)
 
+// direct-to-LDS streaming variants, lanes per row L = 2^LS fixed at compile time:
+// cima_gemv_<fmt>_l<L>_i<IT>_<f32|f16>_dma<D>[_pair][_epi], ..._f16_dma<D>_att_epi, ..._f16_dma<D>_amax
+#define GEMV_KERNEL_D(NAME, F, IT, ACT, PAIR, EPI, XS, AMAX, LS, DD)                               \
+    extern "C" __global__ __launch_bounds__(GNT) void NAME(                                       \
+        const void* x, const uint8_t* wa, const uint8_t* wb, const void* bias_a,                  \
+        const void* bias_b, void* y, int n, int k, int mode, int lpr_shift, GemvExt ext) {       \
+        gemv_body<F, 1, IT, ACT, PAIR, EPI, XS, AMAX, 3, LS, DD>(x, wa, wb, bias_a, bias_b, y, n, \
+                                                                 k, mode, lpr_shift, ext);       \
+    }
+// name: cima_gemv_<fmt>_l<L>_i<IT>_<act>_dma<D>[...], D items in flight per wave
+#define GEMV_DMA_ACT(FN, F, L, LS, IT, ACT, AN, D)                                                             \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_##AN##_dma##D, F, IT, ACT, 0, 0, 0, 0, LS, D)                 \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_##AN##_dma##D##_epi, F, IT, ACT, 0, 1, 0, 0, LS, D)           \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_##AN##_dma##D##_pair, F, IT, ACT, 1, 0, 0, 0, LS, D)          \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_##AN##_dma##D##_pair_epi, F, IT, ACT, 1, 1, 0, 0, LS, D)
+#define GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, D)                                                                  \
+    GEMV_DMA_ACT(FN, F, L, LS, IT, ACT_F32, f32, D) GEMV_DMA_ACT(FN, F, L, LS, IT, ACT_F16, f16, D)             \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma##D##_att_epi, F, IT, ACT_F16, 0, 1, 1, 0, LS, D)      \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma##D##_amax, F, IT, ACT_F16, 0, 0, 0, 1, LS, D)
+#define GEMV_DMA_SHAPE(FN, F, L, LS, IT) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 1) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 2)
+#define GEMV_DMA(FN, F)                                                                                 \
+    GEMV_DMA_SHAPE(FN, F, 64, 6, 1) GEMV_DMA_SHAPE(FN, F, 64, 6, 2) GEMV_DMA_SHAPE(FN, F, 32, 5, 1)       \
+    GEMV_DMA_SHAPE(FN, F, 16, 4, 1)
+
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \
     GEMV_ACT(FN, F, 1, 1) GEMV_ACT(FN, F, 1, 2) GEMV_ACT(FN, F, 1, 4) GEMV_ACT(FN, F, 1, 8)   \
-    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F)
+    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F) GEMV_DMA(FN, F)
 
 // the formats of this code object: the file is compiled once per set (in
 // parallel), each set to its own code object
@@ -1107,6 +1462,8 @@ GEMV_FMT(q4_k, IQ4_K)
 #elif CIMA_GEMV_SET == 1
 GEMV_FMT(q6_k, IQ6_K)
 GEMV_FMT(q5_k, IQ5_K)
+#elif CIMA_GEMV_SET == 3
+// no kernels: a translation unit that includes this file instantiates its own
 #else
 GEMV_FMT(q4_1, IQ4_1)
 GEMV_FMT(q5_0, IQ5_0)

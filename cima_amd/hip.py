@@ -34,7 +34,7 @@ EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_use_own_stream",
     "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
-    "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
+    "cima_hip_set_gemv_dma", "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
@@ -102,6 +102,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_is_fatal.argtypes = [I]
     L.cima_hip_num_cu.argtypes = [P]
     L.cima_hip_set_gemv_tuning.argtypes = [P, I, I]
+    L.cima_hip_set_gemv_dma.argtypes = [P, I]
     L.cima_hip_set_gemv_grid.argtypes = [P, I]
     L.cima_hip_set_gemm_tile.argtypes = [P, I]
     L.cima_hip_gguf_gemv.argtypes = [P, I, P, P, P, P, I, I, I, I]
@@ -224,6 +225,10 @@ class HipCtx:
         """Override the GEMV launch plan (0, 0 = built-in heuristic)."""
         self._check(self.lib.cima_hip_set_gemv_tuning(self.handle, rows, lanes_per_row))
 
+    def set_gemv_dma(self, mode: int = 0) -> None:
+        """GEMV main loop: 0 = heuristic, 1 = direct-to-LDS streaming where built, 2 = register loops."""
+        self._check(self.lib.cima_hip_set_gemv_dma(self.handle, int(mode)))
+
     def set_gemm_tile(self, tokens: int = 0) -> None:
         """Prefill GEMM token-tile width (16, 32, 64, 128 or 256; 0 = built-in choice)."""
         self._check(self.lib.cima_hip_set_gemm_tile(self.handle, int(tokens)))
@@ -284,11 +289,12 @@ class HipCtx:
                                                      int(slab_bytes)))
 
     @staticmethod
-    def nf4_slab_bytes(m: int, n: int, k: int, x_f16: bool = False, workspace: int = 32 << 20) -> int:
-        """Slab size for ``nf4_gemm_slab``: W and (unless X is f16) X as
-        f16, each rounded up to 256 bytes, plus the library workspace."""
-        r = lambda v: (v + 255) // 256 * 256  # noqa: E731
-        return r(2 * n * k) + (0 if x_f16 else r(2 * m * k)) + workspace
+    @staticmethod
+    def nf4_slab_bytes(m: int, n: int, k: int, x_f16: bool = False) -> int:
+        """Slab size with which ``nf4_gemm_slab``'s slab route decodes W in
+        one slice (W as f16); the fused route needs none.  ``m`` and
+        ``x_f16`` are kept for callers written for a slab that also held X."""
+        return (2 * n * k + 255) // 256 * 256
 
     def gguf_dequant(self, fmt: int, src, out, nblocks: int) -> None:
         """Decode ``nblocks`` blocks to f16 (bit-exact with the host decoders)."""
@@ -316,8 +322,9 @@ class HipCtx:
     def nf4_gemm_slab(self, x, packed, absmax, qmap, y, m: int, n: int, k: int, blocksize: int, slab,
                       slab_bytes: Optional[int] = None, x_dtype: Optional[int] = None,
                       y_dtype: Optional[int] = None) -> None:
-        """WTensor::gemm for an NF4 weight (src/quant.rs:131-162): ``Y[m, n] = X . W^T``,
-        W decoded into the f16 ``slab`` and multiplied by hipBLASLt."""
+        """WTensor::gemm for an NF4 weight (src/quant.rs:131-162): ``Y[m, n] = X . W^T``
+        on this library's f16-MFMA tiles, W decoded inside them (or, for shapes
+        they do not take, into the f16 ``slab`` first)."""
         xd, yd = self._gemm_dtypes(x, y, x_dtype, y_dtype)
         if slab_bytes is None:
             slab_bytes = slab.numel() * slab.element_size()

@@ -251,11 +251,11 @@ class Nf4Weight:
 
     def gemm(self, ctx, x, y, scratch=None) -> None:
         """WTensor::gemm for a packed weight (src/quant.rs:131-162): y[m, n] = x[m, k] . W^T.
-        m == 1 runs the fused GEMV; m > 1 dequantises into the ``scratch``
-        slab a row slice at a time and multiplies each slice with the
-        library GEMM (cima_hip_nf4_gemm_slab); any slab that holds one slice
-        works (the reference's is 32 MiB), ``HipCtx.nf4_slab_bytes(m, n,
-        k)`` bytes decode W in one slice."""
+        m == 1 runs the fused GEMV; m > 1 runs cima_hip_nf4_gemm_slab: the
+        f16-MFMA prefill tiles decode W themselves for every checkpoint
+        shape, other shapes decode it into the ``scratch`` slab a row slice
+        at a time; any slab that holds one slice works (the reference's is
+        32 MiB), ``HipCtx.nf4_slab_bytes(m, n, k)`` bytes hold W whole."""
         m = x.shape[0] if x.dim() == 2 else 1
         n, k = y.shape[-1], x.shape[-1]
         self._check_shape(n, k)

@@ -6,10 +6,8 @@
  * src/cuda.rs), with the same argument order and meaning.  Pointers are
  * device pointers (hipMalloc'd or any HIP-visible device memory), sizes are
  * element or row counts, and every call is asynchronous on the context's
- * stream.  No call allocates device memory, so all are safe inside HIP
- * graph capture once the context exists -- except the first
- * cima_hip_nf4_gemm_slab call of each shape, which creates hipBLASLt's
- * handle and plan (make it once before capturing).
+ * stream.  No call allocates device memory or calls a library kernel, so
+ * all are safe inside HIP graph capture once the context exists.
  *
  * Return value: 0 on success; a positive hipError_t when the HIP runtime
  * failed; a negative CIMA_E_* code when the arguments were rejected before
@@ -50,7 +48,7 @@ extern "C" {
 #define CIMA_E_FORMAT -2      /* not a supported GGUF block format */
 #define CIMA_E_NO_KERNEL -3   /* code object lacks the kernel */
 #define CIMA_E_NOT_INIT -4    /* null or destroyed context */
-#define CIMA_E_LIBRARY -5     /* hipBLASLt absent or refused a call (the *_gemm_slab entry points) */
+#define CIMA_E_LIBRARY -5     /* kept for the reference's error set; no entry point returns it now */
 
 typedef struct cima_hip_ctx cima_hip_ctx;
 
@@ -100,6 +98,14 @@ int cima_hip_num_cu(cima_hip_ctx* ctx);
  * values at cima_hip_init (CIMA_GEMV_RING=1 / 2 forces / forbids the
  * item-ring main loop for one-unit rows). */
 int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
+
+/* GEMV main-loop choice (no counterpart in the reference): 0 = built-in
+ * heuristic, 1 = the direct-to-LDS streaming kernels with one item in flight
+ * per wave wherever they are built and fit, 3 = the same with two, 2 =
+ * never them (the register-ring kernels).  Environment variable
+ * CIMA_GEMV_DMA at init.  A set_gemv_tuning override of rows or lanes also
+ * selects the register kernels. */
+int cima_hip_set_gemv_dma(cima_hip_ctx* ctx, int mode);
 
 /* GEMV grid tuning (no counterpart in the reference): the persistent grid
  * holds at most this many 256-thread workgroups per CU (0 = the default of 1, or fewer
@@ -384,16 +390,17 @@ int cima_hip_nf4_gemv(cima_hip_ctx* ctx, const void* x, const void* packed, cons
 int cima_hip_set_nf4_tuning(cima_hip_ctx* ctx, int rows, int kernel);
 /* Prefill GEMM over the packed weight, Y[m, n] (row stride n) = X[m, k] .
  * W[n, k]^T: WTensor::gemm's Nf4 arm (src/quant.rs:131-162), which runs
- * nf4_dequant into the engine's slab, then gemm_f16.  Here X (f32 / bf16)
- * is rounded to f16 at the head of the caller's 256-byte aligned slab, and
- * W is decoded bit-exactly (cima_hip_nf4_dequant) into the rest a row
- * slice at a time -- as many rows as fit beside a workspace of 1/8 of it
- * (at most 32 MiB), slices starting on absmax block boundaries -- each
- * slice multiplied by hipBLASLt (fp32 accumulation) into its columns of
- * Y, as the reference works through its 32 MiB DQ_SCRATCH
- * (src/models/transformer.rs:630-653).  k % 8 == 0, x 16-byte aligned;
- * CIMA_E_INVALID if the slab holds no slice, CIMA_E_LIBRARY if hipBLASLt
- * is absent or has no algorithm for the shape. */
+ * nf4_dequant into the engine's slab, then gemm_f16.  Here, for every
+ * bitsandbytes checkpoint shape (k % 64 == 0, blocksize % 32 == 0, packed
+ * 16-byte aligned) the f16-MFMA prefill tiles of cima_hip_gguf_gemm decode
+ * W themselves -- each weight bit-exactly f16(code * absmax), X rounded to
+ * f16, fp32 accumulation -- and the slab is not touched.  Any other shape
+ * (k % 8 == 0) decodes W into the caller's 256-byte aligned slab one row
+ * slice at a time (slices starting on absmax block boundaries, as the
+ * reference works through its 32 MiB DQ_SCRATCH,
+ * src/models/transformer.rs:630-653) and multiplies each slice with this
+ * library's f16-weight GEMM into its columns of Y.  x 16-byte aligned;
+ * CIMA_E_INVALID if the slab holds no slice. */
 int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed, const float* absmax,
                            const float* qmap, void* y, int m, int n, int k, int blocksize, int x_dtype,
                            int y_dtype, void* slab, unsigned long long slab_bytes);

@@ -162,7 +162,7 @@ def test_gemv_double_quantised_from_safetensors(hip, tmp_path):
     torch.cuda.synchronize()
     want = oracle.nf4_gemv(h.packed, h.absmax, h.qmap, x.float().cpu().numpy(), n, k, bs, threads=8)
     assert rel(y.float().cpu().numpy(), want) < 1e-3
-    # prefill: dequant into the scratch slab + library GEMM
+    # prefill: the MFMA prefill tiles (the scratch slab is checked, not used)
     m = 5
     xs = torch.randn(m, k, device="cuda", dtype=torch.float16)
     ys = torch.empty(m, n, device="cuda", dtype=torch.float16)
@@ -226,12 +226,16 @@ TDT = {0: torch.float32, 1: torch.float16, 2: torch.bfloat16}
 
 
 @pytest.mark.parametrize("m, n, k, bs", [(2, 256, 512, 64), (17, 320, 1024, 128), (300, 512, 2048, 64),
+                                         (40, 200, 4096, 4096), (5, 96, 640, 96), (33, 192, 384, 48),
                                          (9, 130, 200, 20)])
 def test_gemm_slab_parity(hip, m, n, k, bs):
     """cima_hip_nf4_gemm_slab (WTensor::gemm's Nf4 arm, src/quant.rs:131-162)
     against the CPU path: the oracle's bit-exact f16 W times the f16-rounded X
     in float64; 1e-5 with fp32 Y (only the summation order differs), the
-    north star's 1e-3 with f16 Y."""
+    north star's 1e-3 with f16 Y.  The first five shapes take the fused
+    route (the tiles decode W; blocksize 96 is not a power of two), the
+    sixth the slab route's f16-weight tiles (blocksize 48 splits 32-element
+    runs), the last the slab route's plain kernel (k % 64 != 0)."""
     packed, absmax, qmap = case(700 + m, n * k, bs, code=RANDOM_CODE)
     w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(packed, absmax, qmap, n * k, bs)).reshape(n, k)
     xf = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
@@ -266,27 +270,47 @@ def test_gemm_slab_argument_errors(hip):
 
 
 def test_gemm_slab_row_slices(hip):
-    """A slab far smaller than the f16 weight (the reference's 32 MiB
-    DQ_SCRATCH against a 14336 x 4096 weight's 117 MB): W is decoded and
-    multiplied a row slice at a time, each slice writing its columns of Y;
-    the result matches the one-slice run (the library may pick another
-    algorithm per slice shape, so up to summation order) and the CPU path
-    to 1e-5 on sampled rows.  A blocksize that does not divide k makes the
-    slices start on absmax block boundaries."""
-    for n, k, bs, m, slab_mb in ((14336, 4096, 64, 16, 32), (600, 192, 256, 5, 0.1)):
+    """The slab route with a slab far smaller than the f16 weight: W is
+    decoded and multiplied a row slice at a time, each slice writing its
+    columns of Y; the result equals the one-slice run bit for bit (same
+    kernels, same per-row summation) and the CPU path to 1e-5.  Blocksizes
+    that do not divide k make the slices start on absmax block boundaries;
+    one slab holds exactly one slice."""
+    for n, k, bs, m, slab_bytes in ((600, 192, 48, 5, 100 << 10), (300, 200, 20, 7, 40 << 10),
+                                    (96, 320, 80, 3, 2 * 320 * 4)):
         packed, absmax, qmap = case(900 + n, n * k, bs, code=RANDOM_CODE)
         p, a, q = dev(packed), dev(absmax), dev(qmap)
         x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
-        small = torch.empty(int(slab_mb * (1 << 20)), dtype=torch.uint8, device="cuda")
+        small = torch.empty(slab_bytes, dtype=torch.uint8, device="cuda")
         big = torch.empty(hip.nf4_slab_bytes(m, n, k), dtype=torch.uint8, device="cuda")
         ys = torch.empty((m, n), device="cuda")
         yb = torch.empty((m, n), device="cuda")
         hip.nf4_gemm_slab(x, p, a, q, ys, m, n, k, bs, small)
         hip.nf4_gemm_slab(x, p, a, q, yb, m, n, k, bs, big)
         torch.cuda.synchronize()
-        assert rel(ys.cpu().numpy(), yb.cpu().numpy()) <= 1e-6, (n, k)
-        rows = np.random.default_rng(n).choice(n, min(n, 128), replace=False)
+        assert np.array_equal(ys.cpu().numpy(), yb.cpu().numpy()), (n, k)
         w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(packed, absmax, qmap, n * k, bs)).reshape(n, k)
         xh = x.float().cpu().numpy().astype(np.float16).astype(np.float64)
-        want = xh @ w16[rows].astype(np.float64).T
-        assert rel(ys.cpu().numpy()[:, rows], want) <= 1e-5, (n, k)
+        assert rel(ys.cpu().numpy(), xh @ w16.astype(np.float64).T) <= 1e-5, (n, k)
+
+
+@pytest.mark.parametrize("m", [16, 128, 512])
+def test_gemm_fused_full_shape(hip, m):
+    """The fused NF4 prefill at the Llama-3-8B gate/up shape (14336 x 4096,
+    blocksize 64), every output row, against the oracle's bit-exact f16 W
+    times the f16-rounded bf16 X in float64 (1e-5, fp32 Y); the caller's
+    slab is left as it was."""
+    n, k, bs = 14336, 4096, 64
+    packed, absmax, qmap = case(77, n * k, bs)
+    w16 = oracle.f16_bits_to_f32(oracle.nf4_dequant(packed, absmax, qmap, n * k, bs)).reshape(n, k)
+    x = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+    y = torch.full((m, n), float("nan"), device="cuda")
+    slab = torch.full((1 << 20,), 0x5A, dtype=torch.uint8, device="cuda")
+    hip.nf4_gemm_slab(x, dev(packed), dev(absmax), dev(qmap), y, m, n, k, bs, slab)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert not np.isnan(got).any()
+    xh = x.float().cpu().numpy().astype(np.float16).astype(np.float64)
+    want = xh @ w16.astype(np.float64).T
+    assert rel(got, want) <= 1e-5
+    assert bool((slab == 0x5A).all())
