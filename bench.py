@@ -182,6 +182,8 @@ def main():
 
     per_shape = {}
     read_us = {}
+    read_cfg = {}
+    SWEEP_SHAPES = ("q4_k 14336x4096 (gate/up)", "q8_0 14336x4096 (gate/up)", "q4_k 4096x4096 (q/o)")
     hot_us = {}
     gemm_flops = {}
     # the roofline kernel: fused gate+up SwiGLU, cold over the 32 layers
@@ -198,7 +200,27 @@ def main():
     for b in rbufs:
         b.fill_(1)
     sink = torch.zeros(1, dtype=torch.int32, device=dev)
-    pair_read_us = time_calls(lambda b: ctx.stream_read(b, rbytes, sink), rbufs)
+    # read-ceiling sweep: loads in flight per lane, load width, registers or
+    # LDS (global_load_lds_dwordx4) and workgroups per CU; a GEMV is held
+    # against the best of them (cima_hip_stream_read_cfg)
+    READ_CFGS = [(0, 2, 16, 2), (0, 4, 16, 1), (0, 4, 16, 2), (0, 4, 16, 4), (0, 8, 16, 1), (0, 8, 16, 2),
+                 (0, 16, 16, 1), (0, 8, 8, 2), (0, 16, 8, 2), (1, 4, 16, 2), (1, 8, 16, 1), (1, 16, 16, 1)]
+
+    def cfg_name(c):
+        return (f"reg {c[1]}x{c[2]}B" if c[0] == 0 else f"lds ring {c[1]} KB/wave") + f", {c[3]} wg/CU"
+
+    def read_best(bufs, nb, calls=64, keep=None):
+        best = None
+        for c in READ_CFGS:
+            us = time_calls(lambda b: ctx.stream_read_cfg(b, nb, sink, *c), bufs, calls=calls)
+            if keep is not None:
+                keep[cfg_name(c)] = round(us, 3)
+            if best is None or us < best[0]:
+                best = (us, cfg_name(c))
+        return best
+
+    read_sweep = {}
+    pair_read_us, pair_read_cfg = read_best(rbufs, rbytes, keep=read_sweep.setdefault("q4_k 2x14336x4096 (66 MB)", {}))
     del rbufs
     # the device's sustained read bandwidth, re-measured: the same read kernel
     # over 1 GiB transfers (two buffers, so nothing is served from cache)
@@ -217,13 +239,14 @@ def main():
             bufs = [torch.from_numpy(w).to(dev) for _ in range(ncopy)]
             xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev)
             ys = torch.empty(n, device=dev)
-            calls = max(16, min(64, 2 * ncopy))
+            calls = 64  # the copies are cycled, so each call still reads cold weights
             us = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs, calls=calls)
             per_shape[name] = (us, wbytes(t, n, k) + 4 * (n + k))
             hot_us[name] = time_calls(lambda b: ctx.gguf_gemv(t, xs, b, None, ys, n, k, 0), bufs[:1], calls=calls)
-            # the streaming-read time of the same weight bytes, same method
+            # the best streaming-read time of the same weight bytes, same method
             rb = w.nbytes // 16 * 16
-            read_us[name] = time_calls(lambda b: ctx.stream_read(b, rb, sink), bufs, calls=calls)
+            read_us[name], read_cfg[name] = read_best(bufs, rb, calls=calls, keep=read_sweep.setdefault(
+                f"{w.nbytes / 1e6:.1f} MB", {}) if name in SWEEP_SHAPES else None)
             return us
         for nm, (n, k) in [("q4_k 6144x4096 (q|k|v)", (HID + 2 * KV, HID)),
                            ("q4_k 14336x4096 (gate/up)", (FFN, HID)), ("q4_k 4096x14336 (down)", (HID, FFN)),
@@ -249,13 +272,13 @@ def main():
             qm = torch.from_numpy(nf4.NF4_CODE).to(dev)
             xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev).half()
             ys = torch.empty(n, device=dev, dtype=torch.float16)
-            calls = max(16, min(64, 2 * ncopy))
+            calls = 64
             us = time_calls(lambda b: ctx.nf4_gemv(xs, b, b[n * k // 2:].view(torch.float32), qm, ys, n, k, bs),
                             bufs, calls=calls)
             per_shape[name] = (us, nb + 2 * (n + k))
             hot_us[name] = time_calls(lambda b: ctx.nf4_gemv(xs, b, b[n * k // 2:].view(torch.float32), qm, ys, n, k,
                                                              bs), bufs[:1], calls=calls)
-            read_us[name] = time_calls(lambda b: ctx.stream_read(b, nb // 16 * 16, sink), bufs, calls=calls)
+            read_us[name], read_cfg[name] = read_best(bufs, nb // 16 * 16, calls=calls)
         for nm, (n, k) in [("nf4 14336x4096 (gate/up)", (FFN, HID)), ("nf4 4096x14336 (down)", (HID, FFN)),
                            ("nf4 4096x4096 (q/o)", (HID, HID))]:
             nf4_leg(nm, n, k)
@@ -276,6 +299,39 @@ def main():
             hot_us[f"q4_k gemm 14336x4096 m={m} (config 4)"] = time_calls(
                 lambda b: ctx.gguf_gemm_slab(Q4_K, gx, b, gy, m, FFN, HID, gslab), gbufs[:1], calls=24)
             gemm_flops[f"q4_k gemm 14336x4096 m={m} (config 4)"] = 2.0 * FFN * HID * m
+        del gbufs
+        # the same prefill over bitsandbytes NF4 weights (blocksize 64): the
+        # MFMA tiles decode the packed weight themselves
+        nn, kk, bs = FFN, HID, 64
+        nb = nn * kk // 2 + nn * kk // bs * 4
+        g = torch.Generator(device=dev)
+        g.manual_seed(5)
+        nbufs = []
+        for _ in range(12):
+            b = torch.randint(0, 256, (nb,), dtype=torch.uint8, device=dev, generator=g)
+            b[nn * kk // 2:].view(torch.float32).uniform_(0.01, 0.05, generator=g)
+            nbufs.append(b)
+        qm = torch.from_numpy(nf4.NF4_CODE).to(dev)
+        for m in (16, 128, 512):
+            gx = torch.from_numpy(synth.normal(302, 1.0, m * HID)).to(dev).to(torch.bfloat16).reshape(m, HID)
+            gy = torch.empty((m, FFN), device=dev)
+            leg = f"nf4 gemm 14336x4096 m={m} (bitsandbytes prefill)"
+            fn = lambda b: ctx.nf4_gemm_slab(gx, b, b[nn * kk // 2:].view(torch.float32), qm, gy, m, nn, kk, bs, gslab)  # noqa: E731
+            per_shape[leg] = (time_calls(fn, nbufs, calls=24), nb + 2 * m * HID + 4 * m * FFN)
+            hot_us[leg] = time_calls(fn, nbufs[:1], calls=24)
+            gemm_flops[leg] = 2.0 * FFN * HID * m
+        del nbufs
+        # the Q8_0 gate+up pair (the direct-to-LDS streaming kernels)
+        q8g = synth.weights(Q8_0, 310, 0.02, FFN, HID)
+        q8u = synth.weights(Q8_0, 311, 0.02, FFN, HID)
+        qb = [(torch.from_numpy(q8g).to(dev), torch.from_numpy(q8u).to(dev)) for _ in range(6)]
+        xq = torch.from_numpy(synth.normal(9, 1.0, HID)).to(dev)
+        yq = torch.empty(FFN, device=dev)
+        fn = lambda b: ctx.gguf_gemv_swiglu(Q8_0, xq, b[0], b[1], None, None, yq, FFN, HID)  # noqa: E731
+        per_shape["q8_0 gate+up swiglu 2x14336x4096"] = (time_calls(fn, qb, calls=24),
+                                                         2 * wbytes(Q8_0, FFN, HID) + 4 * (HID + FFN))
+        hot_us["q8_0 gate+up swiglu 2x14336x4096"] = time_calls(fn, qb[:1], calls=24)
+        del qb
 
     shapes_out = {}
     for name, (us, b) in per_shape.items():
@@ -286,6 +342,7 @@ def main():
             shapes_out[name]["hot_us_per_call"] = round(hot_us[name], 3)
         if name in read_us:
             shapes_out[name]["read_ceiling_us"] = round(read_us[name], 3)
+            shapes_out[name]["read_ceiling_cfg"] = read_cfg[name]
             shapes_out[name]["frac_of_read_ceiling"] = round(read_us[name] / us, 4)
         if name in gemm_flops:
             tf = gemm_flops[name] / us / 1e6
@@ -304,7 +361,7 @@ def main():
                 "kernel": "cima_gemv_q4_k_r1_i1_f32_ring_pair", "alg_bytes_per_launch": pair_bytes,
                 "avg_launch_us": round(pair_us, 3),
                 "hot_us": round(hot_us["q4_k gate+up swiglu 2x14336x4096"], 3),
-                "read_ceiling_gb_s": round(rbytes / pair_read_us / 1e3, 1),
+                "read_ceiling_gb_s": round(rbytes / pair_read_us / 1e3, 1), "read_ceiling_cfg": pair_read_cfg,
                 "frac_of_read_ceiling": round(achieved / (rbytes / pair_read_us / 1e3), 4),
                 "peak_measured_gb_s": round(peak_measured, 1),
                 "frac_of_measured_peak": round(achieved / peak_measured, 4),
@@ -436,6 +493,7 @@ def main():
                    "ms_per_step_min_max": [round(min(rep_ms) / steps, 5), round(max(rep_ms) / steps, 5)],
                    "timing": "median of --repeats graph replays of exactly --steps layer steps"},
         "shapes": shapes_out,
+        "read_ceiling_sweep_us": read_sweep,
         "decode_step": decode,
         "roofline": roofline,
         "cpu_baseline": cpu,

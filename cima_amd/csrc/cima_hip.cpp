@@ -125,6 +125,10 @@ struct cima_hip_ctx {
     // (cima_hip_attn_decode_noalloc), found by name at init
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // this context's copy of the GEMM code object's X range flags
+    // (cima_gemm_status, read by cima_hip_gemm_status)
+    unsigned* gemm_status = nullptr;
+    bool gemm_xcheck = true;  // CIMA_GEMM_XCHECK=0 at init switches the X range check off
 };
 
 namespace {
@@ -294,9 +298,14 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (!x || !wa || !y || (pair && !wb)) return fail(CIMA_E_INVALID, "%s: null x, w or y", api);
     if (norm_w && (!aligned(norm_w, 16) || !(eps >= 0.f)))
         return fail(CIMA_E_INVALID, "%s: norm weight must be 16-byte aligned and eps >= 0", api);
-    if (!aligned(x, 16) || !aligned(y, 4) || !aligned(wa, F->w_align) || (pair && !aligned(wb, F->w_align)))
-        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x needs 16 B, %s weights %d B)", api, F->name,
-                    F->w_align);
+    // x and y need only their element alignment, as the reference's f16
+    // pointers do (src/cuda.rs:2161): x is read with 16-byte loads that
+    // gfx950 serves at any 2-byte alignment (its unaligned-access mode, the
+    // same the Q8_0 / Q6_K block loads rely on)
+    const uintptr_t es = act == CIMA_DT_F32 ? 4 : 2;
+    if (!aligned(x, es) || !aligned(y, es) || !aligned(wa, F->w_align) || (pair && !aligned(wb, F->w_align)))
+        return fail(CIMA_E_INVALID, "%s: misaligned pointer (x and y need %d B, %s weights %d B)", api, (int)es,
+                    F->name, F->w_align);
     if ((long long)n * (long long)(k / F->block_elems) * F->block_bytes > (1LL << 40))
         return fail(CIMA_E_INVALID, "%s: weight of %d x %d is beyond the supported size", api, n, k);
     GemvPlan p = plan_gemv(ctx, F, n, k, pair);
@@ -439,6 +448,13 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
         }
         ctx->scratch = (void*)sp;
         ctx->scratch_bytes = sb;
+        if ((e = hipModuleGetGlobal(&sp, &sb, ctx->modules[MOD_GEMM], "cima_gemm_status")) != hipSuccess ||
+            sb != sizeof(unsigned)) {
+            unload(ctx);
+            delete ctx;
+            return fail(e != hipSuccess ? (int)e : CIMA_E_NO_KERNEL, "hipModuleGetGlobal(cima_gemm_status) failed");
+        }
+        ctx->gemm_status = (unsigned*)sp;
     }
     // resolve every kernel up front (the reference's KernelSet)
     auto add = [&](int mod, const std::string& name) -> int {
@@ -515,6 +531,11 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                     }
                 }
     if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
+    for (const char* kn : {"cima_stream_read_r1_w16", "cima_stream_read_r2_w16", "cima_stream_read_r4_w16",
+                           "cima_stream_read_r8_w16", "cima_stream_read_r16_w16", "cima_stream_read_r4_w8",
+                           "cima_stream_read_r8_w8", "cima_stream_read_r16_w8", "cima_stream_read_l2",
+                           "cima_stream_read_l4", "cima_stream_read_l8", "cima_stream_read_l16"})
+        if (!rc) rc = add(MOD_DEQUANT, kn);
     for (const char* kn : {"cima_nf4_dequant_v", "cima_nf4_dequant_e", "cima_nf4_gemv_e_f16_f16",
                            "cima_nf4_gemv_e_f32_f32"})
         if (!rc) rc = add(MOD_BNB4, kn);
@@ -545,6 +566,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_RING")) ctx->tune_ring = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_DMA")) ctx->tune_dma = atoi(s);
+    if (const char* s = getenv("CIMA_GEMM_XCHECK")) ctx->gemm_xcheck = atoi(s) != 0;
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -626,6 +648,22 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens) {
     for (int b : kGemmBN) ok = ok || tokens == b;
     if (!ok) return fail(CIMA_E_INVALID, "cima_hip_set_gemm_tile: %d is not 0, 16, 32, 64, 128 or 256", tokens);
     ctx->tune_gemm_bn = tokens;
+    return 0;
+}
+
+int cima_hip_gemm_status(cima_hip_ctx* ctx, unsigned int* flags, int clear) {
+    const char* api = "cima_hip_gemm_status";
+    if (!ctx || !ctx->loaded) return fail(CIMA_E_NOT_INIT, "%s: context is not initialised", api);
+    if (!flags) return fail(CIMA_E_INVALID, "%s: null flags", api);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, api);
+    if ((e = hipMemcpy(flags, ctx->gemm_status, sizeof(unsigned), hipMemcpyDeviceToHost)) != hipSuccess)
+        return hip_fail(e, api);
+    if (clear) {
+        const unsigned zero = 0;
+        if ((e = hipMemcpy(ctx->gemm_status, &zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess)
+            return hip_fail(e, api);
+    }
     return 0;
 }
 
@@ -744,6 +782,7 @@ struct GemmExt {
     const float* qmap;
     long long bsz;
     int bs_shift;
+    unsigned* status;
 };
 
 // Launches cima_gemm_<fname>_b<BN>[n]_<x>_<y> over Y[m, n] (row stride ldy):
@@ -776,6 +815,7 @@ int gemm_launch(cima_hip_ctx* ctx, const char* fname, const void* x, const void*
     void* ya = y;
     int mm = m, nn = n, kk = k, ld = ldy;
     GemmExt ge = gext;
+    ge.status = ctx->gemm_xcheck ? ctx->gemm_status : nullptr;
     void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld, &ge};
     const unsigned threads = bn == 16 && !narrow ? 512 : 256;
     hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, threads, 1,
@@ -1190,16 +1230,46 @@ int cima_hip_graph_destroy(cima_hip_graph* g) {
     return 0;
 }
 
+int cima_hip_stream_read_cfg(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink, int dest,
+                             int depth, int width, int wgs_per_cu) {
+    const char* api = "cima_hip_stream_read_cfg";
+    if (int rc = ready(ctx, api)) return rc;
+    if (nbytes < 0 || !src || !sink || !aligned(src, 16))
+        return fail(CIMA_E_INVALID, "%s: null or misaligned (16 B) pointer, or nbytes < 0", api);
+    if (wgs_per_cu < 1 || wgs_per_cu > 8) return fail(CIMA_E_INVALID, "%s: %d workgroups per CU", api, wgs_per_cu);
+    char name[64];
+    long long per_wg;  // bytes one workgroup takes per round
+    if (dest == 0) {
+        const bool ok = (width == 16 && (depth == 1 || depth == 2 || depth == 4 || depth == 8 || depth == 16)) ||
+                        (width == 8 && (depth == 4 || depth == 8 || depth == 16));
+        if (!ok) return fail(CIMA_E_INVALID, "%s: register reads of %d x %d B are not built", api, depth, width);
+        snprintf(name, sizeof name, "cima_stream_read_r%d_w%d", depth, width);
+        per_wg = 256LL * depth * width;
+    } else if (dest == 1) {
+        if (width != 16 || !(depth == 2 || depth == 4 || depth == 8 || depth == 16))
+            return fail(CIMA_E_INVALID, "%s: LDS rings of %d KB per wave are not built", api, depth);
+        snprintf(name, sizeof name, "cima_stream_read_l%d", depth);
+        per_wg = 4LL * 1024 * depth;
+    } else {
+        return fail(CIMA_E_INVALID, "%s: destination %d is not 0 (registers) or 1 (LDS)", api, dest);
+    }
+    if (nbytes < 1024) return 0;
+    long long grid = (nbytes + per_wg - 1) / per_wg;
+    if (grid > (long long)wgs_per_cu * ctx->num_cu) grid = (long long)wgs_per_cu * ctx->num_cu;
+    void* args[] = {&src, &nbytes, &sink};
+    return launch_named(ctx, name, (unsigned)grid, 256, args, api);
+}
+
 int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink) {
     const char* api = "cima_hip_stream_read";
     if (int rc = ready(ctx, api)) return rc;
     if (nbytes < 0 || !src || !sink || !aligned(src, 16))
         return fail(CIMA_E_INVALID, "%s: null or misaligned (16 B) pointer, or nbytes < 0", api);
-    long long n16 = nbytes / 16;
-    if (n16 == 0) return 0;
-    long long grid = (n16 + 4 * 256 - 1) / (4 * 256);
+    nbytes &= ~15LL;
+    if (nbytes == 0) return 0;
+    long long grid = (nbytes / 16 + 4 * 256 - 1) / (4 * 256);
     if (grid > 2L * ctx->num_cu) grid = 2L * ctx->num_cu;
-    void* args[] = {&src, &n16, &sink};
+    void* args[] = {&src, &nbytes, &sink};
     return launch_named(ctx, "cima_stream_read", (unsigned)grid, 256, args, api);
 }
 
@@ -1361,7 +1431,7 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
     if (k % 64 == 0 && blocksize % 32 == 0 && aligned(packed, 16) && aligned(absmax, 4)) {
         const int sh = (blocksize & (blocksize - 1)) == 0 ? log2i(blocksize) : -1;
         return gemm_launch(ctx, "nf4", x, packed, y, m, n, k, n, x_dtype, y_dtype,
-                           GemmExt{absmax, qmap, (long long)blocksize, sh}, api);
+                           GemmExt{absmax, qmap, (long long)blocksize, sh, nullptr}, api);
     }
     // Slab route for the other shapes: W is decoded into the slab a row
     // slice at a time (the reference's lin_gemm works through its 32 MiB

@@ -1,6 +1,8 @@
 // Dequantisation to f16 and packed embedding gather (gfx950 code object
 // cima_dequant.hsaco): one thread per unit of a block, bit-exact with the
 // host decoders (src/quant.rs:599-896).
+#include <type_traits>
+
 #include "gguf_formats.h"
 
 // --------------------------------------------------------- dequant / gather
@@ -53,30 +55,111 @@ DQ_KERNELS(iq4_xs, FIQ4_XS)
 
 
 // ------------------------------------------------------ bandwidth reference
-// Streams n16 16-byte words once (grid-stride, four independent loads in
-// flight per thread) and folds them into a value that is stored only if it
+// Streaming reads that fold the data into a value stored only if it
 // matches an improbable pattern: the plain HBM read ceiling the GEMVs are
-// measured against.
-extern "C" __global__ __launch_bounds__(256) void cima_stream_read(const uint4* __restrict__ src, long long n16,
-                                                                   uint32_t* __restrict__ sink) {
-    // grid-stride, four independent 16-byte nontemporal loads per thread in
-    // flight: of the read patterns measured on MI355X (1-32 loads per
-    // thread, 1-8 workgroups per CU, plain or nontemporal, grid-stride or
-    // per-workgroup slabs) the fastest or within 2% of it at 33, 66 and
-    // 431 MB, with two workgroups per CU
-    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-    const v4u* p = reinterpret_cast<const v4u*>(src);
+// measured against, in a family swept over the three things that set a
+// read's pace on gfx950 -- loads in flight per lane, load width and the
+// destination (registers, or LDS through global_load_lds_dwordx4) -- the
+// host choosing workgroups per CU (cima_hip_stream_read_cfg).
+//
+// Register reads: grid-stride over W-byte words, NL independent loads per
+// thread in flight.
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u_t __attribute__((ext_vector_type(2)));
+template <int NL, int W>
+DEV void stream_read_reg(const uint8_t* __restrict__ src, long long nbytes, uint32_t* __restrict__ sink) {
+    using V = typename std::conditional<W == 16, v4u_t, v2u_t>::type;
+    const V* p = reinterpret_cast<const V*>(src);
+    const long long nw = nbytes / W;
     const long long nt = (long long)gridDim.x * 256;
     long long i = (long long)blockIdx.x * 256 + threadIdx.x;
     uint32_t acc = 0;
-    for (; i + 3 * nt < n16; i += 4 * nt) {
-        const v4u a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + nt);
-        const v4u c = __builtin_nontemporal_load(p + i + 2 * nt), d = __builtin_nontemporal_load(p + i + 3 * nt);
-        acc ^= (a.x + b.y) ^ (c.z + d.w) ^ (a.w + b.x) ^ (c.y + d.z);
+    for (; i + (NL - 1) * nt < nw; i += NL * nt) {
+        V a[NL];
+#pragma unroll
+        for (int j = 0; j < NL; j++) a[j] = __builtin_nontemporal_load(p + i + j * nt);
+#pragma unroll
+        for (int j = 0; j < NL; j++) acc ^= a[j].x + a[j].y;
     }
-    for (; i < n16; i += nt) {
-        const v4u a = __builtin_nontemporal_load(p + i);
-        acc ^= a.x ^ a.w;
+    for (; i < nw; i += nt) {
+        const V a = __builtin_nontemporal_load(p + i);
+        acc ^= a.x ^ a.y;
     }
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
+
+// Direct-to-LDS reads: each wave streams 1 KB runs (64 lanes x 16 B,
+// grid-stride over waves) through a ring of D 1 KB slots in LDS, D copies in
+// flight, each slot read back once (the GEMV's _dma loop without the dot).
+DEV void dma16_rd(const void* g, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+template <int N>
+DEV void wait_vm_rd() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+template <int D>
+DEV void stream_read_lds(const uint8_t* __restrict__ src, long long nbytes, uint32_t* __restrict__ sink) {
+    __shared__ __align__(16) uint8_t ring[4][D * 1024];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const long long nch = nbytes >> 10;  // whole 1 KB runs (the tail < 1 KB is not read)
+    const long long W = (long long)gridDim.x * 4, g = (long long)blockIdx.x * 4 + wave;
+    const long long per = g < nch ? (nch - 1 - g) / W + 1 : 0;
+    const uint32_t base = (uint32_t)(uintptr_t)&ring[wave][0];
+    auto at = [&](long long q) { return src + (min(g + q * W, nch - 1) << 10) + 16 * lane; };
+    uint32_t acc = 0;
+    if (per > 0) {
+#pragma unroll
+        for (int d = 0; d < D; d++) dma16_rd(at(d), base + d * 1024);
+        long long i = 0;
+        for (; i + D <= per; i += D) {
+#pragma unroll
+            for (int d = 0; d < D; d++) {
+                wait_vm_rd<D - 1>();
+                const uint2 v = *reinterpret_cast<const uint2*>(&ring[wave][d * 1024 + 16 * lane]);
+                acc ^= v.x + v.y;
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                dma16_rd(at(i + d + D), base + d * 1024);
+            }
+        }
+        wait_vm_rd<0>();
+        for (int d = 0; i + d < per; d++) {
+            const uint2 v = *reinterpret_cast<const uint2*>(&ring[wave][d * 1024 + 16 * lane]);
+            acc ^= v.x + v.y;
+        }
+    }
+    if (acc == 0x9E3779B9u) sink[0] = acc;
+}
+
+// cima_stream_read: four 16-byte loads in flight per thread (the default
+// of cima_hip_stream_read: of the patterns measured on MI355X, cold, the
+// fastest or within 2% of it at 33, 62 and 431 MB with two workgroups per
+// CU: 6.5 / 10.6 / 63.0 us, against 7.0-9.2 / 11.1-13.7 / 66 us for 8 or 16
+// loads in flight or one workgroup per CU, and 6.9-8.2 / 10.9-12.4 /
+// 68-78 us for direct-to-LDS rings of 8-32 KB per wave)
+extern "C" __global__ __launch_bounds__(256) void cima_stream_read(const uint8_t* __restrict__ src, long long nbytes,
+                                                                   uint32_t* __restrict__ sink) {
+    stream_read_reg<4, 16>(src, nbytes, sink);
+}
+#define STREAM_READ_REG(NL, W)                                                                              \
+    extern "C" __global__ __launch_bounds__(256) void cima_stream_read_r##NL##_w##W(                      \
+        const uint8_t* __restrict__ src, long long nbytes, uint32_t* __restrict__ sink) {                  \
+        stream_read_reg<NL, W>(src, nbytes, sink);                                                          \
+    }
+STREAM_READ_REG(1, 16)
+STREAM_READ_REG(2, 16)
+STREAM_READ_REG(4, 16)
+STREAM_READ_REG(8, 16)
+STREAM_READ_REG(16, 16)
+STREAM_READ_REG(4, 8)
+STREAM_READ_REG(8, 8)
+STREAM_READ_REG(16, 8)
+#define STREAM_READ_LDS(D)                                                                                   \
+    extern "C" __global__ __launch_bounds__(256) void cima_stream_read_l##D(                               \
+        const uint8_t* __restrict__ src, long long nbytes, uint32_t* __restrict__ sink) {                  \
+        stream_read_lds<D>(src, nbytes, sink);                                                               \
+    }
+STREAM_READ_LDS(2)
+STREAM_READ_LDS(4)
+STREAM_READ_LDS(8)
+STREAM_READ_LDS(16)

@@ -211,6 +211,108 @@ struct GemmExt {
     const float* qmap;
     long long bsz;   // elements per absmax entry
     int bs_shift;    // log2(bsz) when bsz is a power of two, else -1
+    unsigned* status;  // X range flags (cima_gemm_status), OR-ed in
+};
+
+// X range report.  The tiles round X to f16.  That is exact for bf16 values
+// of 2^-17 <= |x| < 65536 (and zero); larger ones become +-inf, and smaller
+// nonzero ones may lose bits (f16 subnormals step by 2^-24).  f32 X is
+// rounded anyway (the 1e-3 bar), but |x| >= 65520 becomes inf too.  Every
+// workgroup checks its own 1/(grid size) share of X once (XScan: a few
+// 16-byte words per thread, loaded ahead of the first weight stage) and ORs
+// flags into a word of this code object, which the host reads back on
+// request (cima_hip_gemm_status): bit 0 = values beyond f16's range, or not
+// finite; bit 1 = nonzero bf16 values below 2^-17.  The loads go out after
+// the main loop, beside the output stores, and are checked last.  Measured
+// on MI355X (Q4_K 14336x4096, bf16 X), against no check: +0.8-1.2 / +0.9 /
+// +0.5 / +0.5 / +1-2 us at 16 / 32 / 64 / 128 / 512 tokens (1-6 %);
+// checked before the main loop instead it cost 1.3-2.6 us at 16-32
+// tokens, and inside the tiles' own conversions every stage (+1170 VALU
+// instructions in the 256-token tile, 102 -> 150 us at 512 tokens).
+__device__ unsigned cima_gemm_status;
+struct XRange {
+    // one word of flags, two bf16 halves at a time (magnitudes h <= 0x7fff,
+    // so the additions below never carry out of a half): bit 15 of a half
+    // <- h >= 0x4780 (65536: beyond f16, or inf / NaN); bit 14 <- 0 < h <
+    // 0x3700 (below 2^-17); f32: bit 31 <- |x| >= 65520
+    uint32_t acc = 0;
+    DEV void bf16(uint32_t w) {
+        const uint32_t a = w & 0x7fff7fffu;
+        acc |= ((a + 0x38803880u) & 0x80008000u) | ((~(a + 0x49004900u) & (a + 0x7fff7fffu) & 0x80008000u) >> 1);
+    }
+    DEV void f32(uint32_t w) { acc |= ((w & 0x7fffffffu) + 0x38801000u) & 0x80000000u; }
+    template <int XT>
+    DEV void add(uint4 v) {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if constexpr (XT == XT_BF16) bf16(w[i]);
+            else f32(w[i]);
+        }
+    }
+    DEV void report(unsigned* st) const {
+        const unsigned long long bo = __ballot((acc & 0x80008000u) != 0), bt = __ballot((acc & 0x40004000u) != 0);
+        if ((bo | bt) && (threadIdx.x & 63) == 0 && st) atomicOr(st, (bo ? 1u : 0u) | (bt ? 2u : 0u));
+    }
+};
+
+// This workgroup's share of X for the range check: words [w0, we) of X's
+// 16-byte words, thread t taking w0 + t + T j.  issue() loads the first NB
+// per thread; finish() checks them (and, for large X, the rest, batch by
+// batch) and reports.  Nothing for f16 X.
+typedef uint32_t v4u32_t __attribute__((ext_vector_type(4)));
+template <int XT, int T>  // T: threads per workgroup (a constant: reading blockDim is a load, and a wait)
+struct XScan {
+    static constexpr int NB = 4;
+    v4u32_t v[XT == XT_F16 ? 1 : NB];
+    long long w0 = 0, we = 0;
+    bool on = false;
+    DEV void issue(const void* x, int m, int k, const unsigned* st) {
+        on = st != nullptr;  // uniform: a null status word switches the check off
+        if constexpr (XT != XT_F16) {
+            if (!on) return;
+            const long long nw = (long long)m * k * (XT == XT_F32 ? 4 : 2) / 16;
+            const long long nwg = (long long)gridDim.x * gridDim.y;
+            const long long per = (nw + nwg - 1) / nwg;
+            w0 = ((long long)blockIdx.y * gridDim.x + blockIdx.x) * per;
+            we = min(w0 + per, nw);
+            const uint4* p = static_cast<const uint4*>(x);
+            // Loads in asm: compiled as plain loads, predicated per lane,
+            // they are joined with the lanes that load nothing and waited
+            // for on the spot; in asm they stay in flight beside the output
+            // stores until finish().  Batches the share does not reach
+            // are skipped (a uniform branch); lanes past the share repeat
+            // the share's last word, which their wave's request coalesces
+            // (clamping to one word of X for every workgroup made 448
+            // workgroups queue on one L2 line: +2 us at 16 tokens).
+            const long long last = max(min(we, nw) - 1, 0LL);
+            v[0] = v4u32_t{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                if (w0 + (long long)T * j >= we) break;
+                const long long i = min(w0 + threadIdx.x + (long long)T * j, last);
+                asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v[j]) : "v"(p + i) : "memory");
+            }
+        }
+    }
+    DEV void finish(const void* x, unsigned* st) {
+        if constexpr (XT != XT_F16) {
+            if (!on) return;
+            XRange rg;
+            const uint4* p = static_cast<const uint4*>(x);
+            // the asm loads above are not counted by the compiler: wait for
+            // everything in flight (the tile's first stage, which comes next
+            // anyway) and hand the registers back as defined here
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+                asm volatile("" : "+v"(v[j]));
+                if (w0 + threadIdx.x + (long long)T * j < we) rg.add<XT>(__builtin_bit_cast(uint4, v[j]));
+            }
+            for (long long i = w0 + threadIdx.x + (long long)T * NB; i < we; i += T) rg.add<XT>(p[i]);
+            rg.report(st);
+        }
+    }
 };
 
 // The tile bodies call D::ctx / init / load / deq with a per-call context;
@@ -353,11 +455,12 @@ struct XTile {
                 // ring in scratch memory (the aggregate is not promoted)
                 *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
             } else if constexpr (XT == XT_BF16) {
-                // bf16 -> f16 is exact for 2^-14 <= |x| < 65520
+                // bf16 -> f16 is exact for 2^-17 <= |x| < 65536
                 uint32_t o[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < 4; j++) {
                     o[j] = f2h2(__builtin_bit_cast(float, w[j] << 16), __builtin_bit_cast(float, w[j] & 0xffff0000u));
+                }
                 *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
             } else {
                 *reinterpret_cast<uint2*>(dst) =
@@ -420,6 +523,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
     const auto dc = D::ctx(w, ext);
     fmt_init<D>(dc, ext);
+    XScan<XT, 256> xscan;
     const int nk = k / BK;
     const int wrow = tid >> 1, wsub = tid & 1;
     const uint8_t* wp = w + (size_t)min(r0 + wrow, n - 1) * row_bytes;
@@ -447,8 +551,9 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
             } else if constexpr (XT == XT_BF16) {
                 uint32_t o[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++)
+                for (int j = 0; j < 4; j++) {
                     o[j] = f2h2(__builtin_bit_cast(float, wv[j] << 16), __builtin_bit_cast(float, wv[j] & 0xffff0000u));
+                }
                 *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
             } else {
                 *reinterpret_cast<uint2*>(dst) =
@@ -531,6 +636,7 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
     for (int b0 = 0; b0 < PF - 1; b0++)
         if (base + b0 < nk - 1) step(ring[(b0 + 1) % PF], base + b0, true);
     step(ring[0], nk - 1, false);
+    xscan.issue(x, m, k, ext.status);  // the range check's loads overlap the output stores
 
 #pragma unroll
     for (int a = 0; a < 2; a++) {
@@ -549,6 +655,8 @@ __device__ void gemm_body_pipe(const void* __restrict__ x, const uint8_t* __rest
             }
         }
     }
+
+    xscan.finish(x, ext.status);
 }
 
 // Split-k tiles for up to 16 tokens: a workgroup of 4 RT waves owns 16 RT
@@ -574,6 +682,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
     const auto dc = D::ctx(w, ext);
     fmt_init<D>(dc, ext);
+    XScan<XT, 64 * NW> xscan;
     const int nk = k / 128, cnt = (nk + 3) >> 2;  // every wave runs cnt steps (a uniform barrier count)
     const uint8_t* wp = w + (size_t)min(r0 + 16 * rt + (lane & 15), n - 1) * row_bytes;
     // this lane's share of the split's x tile: E elements of one token
@@ -612,10 +721,11 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
                 const uint32_t v[4] = {st.xr[j].x, st.xr[j].y, st.xr[j].z, st.xr[j].w};
                 uint32_t o[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++)
+                for (int e = 0; e < 4; e++) {
                     o[e] = XT == XT_F16 ? v[e]
                                         : f2h2(__builtin_bit_cast(float, v[e] << 16),
                                                __builtin_bit_cast(float, v[e] & 0xffff0000u));
+                }
                 dst[j] = make_uint4(o[0], o[1], o[2], o[3]);
             }
         }
@@ -644,6 +754,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
     for (int b0 = 0; b0 < PF - 1; b0++)
         if (base + b0 < cnt) step(ring[b0], base + b0, false);
 
+    xscan.issue(x, m, k, ext.status);  // the range check's loads overlap the split reduction
     // lane l holds D[row 4(l/16) + i][token l%16] of its tile; sum the splits
     __syncthreads();
     float* red = reinterpret_cast<float*>(&xl[0][0][0]);  // [NW waves][256]
@@ -661,6 +772,8 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
             else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(v);
         }
     }
+
+    xscan.finish(x, ext.status);
 }
 
 
@@ -684,6 +797,7 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
     const size_t row_bytes = (size_t)(k / D::BE) * D::BB;
     const auto dc = D::ctx(w, ext);
     fmt_init<D>(dc, ext);
+    XScan<XT, 256> xscan;
     const int nk = k / BK;
     const int h = lane >> 5;
 
@@ -750,6 +864,7 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
     for (int b0 = 0; b0 < PF - 1; b0++)
         if (base + b0 < nk) step(ring[b0], base + b0, false);
 
+    xscan.issue(x, m, k, ext.status);  // the range check's loads overlap the output stores
     // lane l, element i of a 32x32 tile: row 8(i/4) + 4(l/32) + i%4, column l%32
 #pragma unroll
     for (int a = 0; a < RA; a++) {
@@ -768,6 +883,8 @@ __device__ void gemm_body_ra(const void* __restrict__ x, const uint8_t* __restri
             }
         }
     }
+
+    xscan.finish(x, ext.status);
 }
 
 
@@ -813,12 +930,16 @@ constexpr int ra_pf() {
 // 16-row split-k tiles (four waves) for weights too narrow to fill the CUs
 // with 32-row tiles: the _b16n_ kernels.  Two stages in flight at three
 // workgroups per CU where a stage's registers allow it without spilling
-// (not for f32 X, eight load words per stage, nor Q6_K), else one at four
+// (not for f32 X, eight load words per stage, nor Q6_K, Q5_K and f16
+// weights, whose stages are the largest), else one at four
 // (measured on MI355X, Q4_K, bf16 X, 16 tokens: 38.8 -> 25.0 us on
 // 4096x14336, 12.9 -> 9.2 on 4096x4096).
 template <typename D, int XT>
 constexpr int sk16n_pf() {
-    return (XT != XT_F32 && !std::is_same<D, GG<DQ6_K>>::value && !std::is_same<D, DF16>::value) ? 2 : 1;
+    return (XT != XT_F32 && !std::is_same<D, GG<DQ6_K>>::value && !std::is_same<D, GG<DQ5_K>>::value &&
+            !std::is_same<D, DF16>::value)
+               ? 2
+               : 1;
 }
 #define GEMM_KERNEL_NARROW(FN, D, XT, XN, YT, YN)                                                   \
     extern "C" __global__ __launch_bounds__(256, (sk16n_pf<D, XT>() == 2 ? 3 : 4)) void            \

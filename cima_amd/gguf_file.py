@@ -260,9 +260,18 @@ def write(path: str, meta: Iterable[tuple], tensors: Iterable[tuple], version: i
 
 # ------------------------------------------------- the decoder in the file
 
-def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128):
+def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128,
+                   use_sliding_window: bool = False):
     """DecoderConfig from the metadata (``model_config``,
-    src/formats.rs:940-1007), for the qwen2 / llama tensor family."""
+    src/formats.rs:940-1007), for the qwen2 / llama tensor family.
+
+    The reference's model_config ignores ``{arch}.attention.sliding_window``
+    for these architectures and always decodes with full causal attention,
+    so by default this loader does too (window 0): a file that carries the
+    key -- one converted from an HF config with use_sliding_window=false,
+    say -- decodes as the reference decodes it.  ``use_sliding_window=True``
+    opts in to the file's single window (a per-layer pattern is refused
+    then rather than decoded with the wrong span)."""
     from .decoder import DecoderConfig
 
     a = g.architecture
@@ -286,10 +295,10 @@ def decoder_config(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 12
         raise GGUFError("blk.0.attn_q.weight is missing -- not a qwen2 / llama-family decoder")
     eps = g.meta_float(f"{a}.attention.layer_norm_rms_epsilon")
     theta = g.meta_float(f"{a}.rope.freq_base")
-    # sliding-window attention: one window for every layer is supported; a
-    # per-layer pattern (alternating local / global layers) is not, and is
-    # refused rather than decoded with the wrong attention span
-    window = g.meta_int(f"{a}.attention.sliding_window") or 0
+    # sliding-window attention, opt-in: one window for every layer is
+    # supported; a per-layer pattern (alternating local / global layers) is
+    # not, and is refused rather than decoded with the wrong attention span
+    window = (g.meta_int(f"{a}.attention.sliding_window") or 0) if use_sliding_window else 0
     if window and any(k.startswith(f"{a}.attention.sliding_window_") for k in g.meta):
         raise GGUFError(f"{a}: per-layer sliding-window patterns are not supported by this decoder")
     return DecoderConfig(
@@ -323,13 +332,15 @@ def _matrix(g: GGUFFile, name: str, rows: int, k: int):
     return g.tensor_data(name), int(ti.ggml_type)
 
 
-def load_model(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128):
+def load_model(g: GGUFFile, max_seq: int | None = None, attn_chunk: int = 128,
+               use_sliding_window: bool = False):
     """The qwen2 / llama-family decoder of a GGUF file as a HostModel, in
     the decode step's layout: q, k, v as one matrix when they share a
-    format (else separate), gate and up as one; norms and biases as f16."""
+    format (else separate), gate and up as one; norms and biases as f16.
+    Full causal attention unless ``use_sliding_window`` (decoder_config)."""
     from .decoder import HostModel
 
-    c = decoder_config(g, max_seq, attn_chunk)
+    c = decoder_config(g, max_seq, attn_chunk, use_sliding_window)
     qd, kvd = c.q_heads * c.head_dim, c.kv_heads * c.head_dim
     embed, et = _matrix(g, "token_embd.weight", c.vocab, c.hidden)
     m = HostModel(c, embed, _f16_vector(g, "output_norm.weight", c.hidden), embed_type=et)

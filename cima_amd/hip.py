@@ -34,7 +34,7 @@ EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_use_own_stream",
     "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
-    "cima_hip_set_gemv_dma", "cima_hip_set_gemv_grid", "cima_hip_set_gemm_tile",
+    "cima_hip_set_gemv_dma", "cima_hip_set_gemv_grid", "cima_hip_gemm_status", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
@@ -42,7 +42,7 @@ EXPORTS = (
     "cima_hip_argmax_to_ids", "cima_hip_pos_bump", "cima_hip_decode_step",
     "cima_hip_capture_begin", "cima_hip_capture_end", "cima_hip_graph_launch", "cima_hip_graph_destroy",
     "cima_hip_nf4_dequant", "cima_hip_nf4_gemv", "cima_hip_set_nf4_tuning", "cima_hip_nf4_gemm_slab",
-    "cima_hip_stream_read",
+    "cima_hip_stream_read", "cima_hip_stream_read_cfg",
 )
 
 
@@ -103,6 +103,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_num_cu.argtypes = [P]
     L.cima_hip_set_gemv_tuning.argtypes = [P, I, I]
     L.cima_hip_set_gemv_dma.argtypes = [P, I]
+    L.cima_hip_gemm_status.argtypes = [P, ctypes.POINTER(ctypes.c_uint), I]
     L.cima_hip_set_gemv_grid.argtypes = [P, I]
     L.cima_hip_set_gemm_tile.argtypes = [P, I]
     L.cima_hip_gguf_gemv.argtypes = [P, I, P, P, P, P, I, I, I, I]
@@ -123,6 +124,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_decode_step.argtypes = [P, ctypes.POINTER(Decoder)]
     L.cima_hip_capture_begin.argtypes = [P]
     L.cima_hip_stream_read.argtypes = [P, P, LL, P]
+    L.cima_hip_stream_read_cfg.argtypes = [P, P, LL, P, I, I, I, I]
     L.cima_hip_nf4_dequant.argtypes = [P, P, P, P, P, LL, I]
     L.cima_hip_nf4_gemv.argtypes = [P, P, P, P, P, P, I, I, I, I]
     L.cima_hip_set_nf4_tuning.argtypes = [P, I, I]
@@ -228,6 +230,14 @@ class HipCtx:
     def set_gemv_dma(self, mode: int = 0) -> None:
         """GEMV main loop: 0 = heuristic, 1 = direct-to-LDS streaming where built, 2 = register loops."""
         self._check(self.lib.cima_hip_set_gemv_dma(self.handle, int(mode)))
+
+    def gemm_status(self, clear: bool = True) -> int:
+        """X range flags of the prefill GEMMs since the last clear (waits for the
+        stream): bit 0 = values beyond f16's range / non-finite, bit 1 = bf16
+        values below 2^-17 (cima_hip_gemm_status)."""
+        v = ctypes.c_uint(0)
+        self._check(self.lib.cima_hip_gemm_status(self.handle, ctypes.byref(v), 1 if clear else 0))
+        return int(v.value)
 
     def set_gemm_tile(self, tokens: int = 0) -> None:
         """Prefill GEMM token-tile width (16, 32, 64, 128 or 256; 0 = built-in choice)."""
@@ -418,6 +428,13 @@ class HipCtx:
     def decode_step(self, desc: "Decoder") -> None:
         """One greedy decode step of a whole decoder (cima_hip_decode_step)."""
         self._check(self.lib.cima_hip_decode_step(self.handle, ctypes.byref(desc)))
+
+    def stream_read_cfg(self, src, nbytes: int, sink, dest: int, depth: int, width: int = 16,
+                        wgs_per_cu: int = 2) -> None:
+        """Read ceiling in a chosen form: dest 0 = registers (depth loads of width
+        bytes per thread), 1 = LDS ring of depth 1 KB copies per wave."""
+        self._check(self.lib.cima_hip_stream_read_cfg(self.handle, _ptr(src), nbytes, _ptr(sink), dest, depth, width,
+                                                      wgs_per_cu))
 
     def stream_read(self, src, nbytes: int, sink) -> None:
         """Read nbytes once (bandwidth reference)."""

@@ -112,6 +112,21 @@ int cima_hip_set_gemv_dma(cima_hip_ctx* ctx, int mode);
  * if fewer fit; environment variable CIMA_GEMV_WGS at init). */
 int cima_hip_set_gemv_grid(cima_hip_ctx* ctx, int wgs_per_cu);
 
+/* X range flags of the prefill GEMMs (no counterpart in the reference).
+ * The MFMA tiles round X to f16: exact for bf16 X of 2^-17 <= |x| < 65536
+ * and zero, while larger values become +-inf and smaller nonzero ones may
+ * lose bits; f32 X of |x| >= 65520 becomes inf.  Every gguf_gemm /
+ * gguf_gemm_slab / nf4_gemm_slab call ORs into a per-context word: bit 0 =
+ * X held values beyond f16's range, inf or NaN; bit 1 = X (bf16) held
+ * nonzero values below 2^-17.  This call waits for the context's stream,
+ * returns the word in *flags and clears it when `clear` is nonzero.  Not
+ * for use during graph capture (it synchronises).  The check reads each X
+ * element once more (its share in every workgroup, from L2); the
+ * environment variable CIMA_GEMM_XCHECK=0 at cima_hip_init switches it off. */
+#define CIMA_XRANGE_OVERFLOW 1u
+#define CIMA_XRANGE_TINY 2u
+int cima_hip_gemm_status(cima_hip_ctx* ctx, unsigned int* flags, int clear);
+
 /* Prefill GEMM tuning (no counterpart in the reference): token-tile width
  * (16, 32, 64, 128 or 256) for later gguf_gemm calls; 0 = the built-in
  * choice (16 up to 32 tokens; 32 up to 128 while that grid has at most one
@@ -131,8 +146,10 @@ int cima_hip_set_gemm_tile(cima_hip_ctx* ctx, int tokens);
  *           src/kernels.cu:493-538)
  *   act_dtype: CIMA_DT_F32 (x, bias, y fp32) or CIMA_DT_F16 (x, bias, y f16,
  *   the engine's activation type).  bias may be NULL.
- * Requires k % 32 == 0 (Q8_0, Q4_0) or k % 256 == 0 (Q4_K, Q6_K), x and y
- * 16-byte aligned, W 16-byte aligned for Q4_K and 2-byte aligned otherwise.
+ * Requires k % 32 == 0 (Q8_0, Q4_0) or k % 256 == 0 (Q4_K, Q6_K); x, bias
+ * and y aligned to their element size (2 bytes f16, 4 bytes f32) as the
+ * reference's pointers are, so a caller may pass a sub-slice at any element
+ * offset; W 16-byte aligned for Q4_K and 2-byte aligned otherwise.
  * Unlike the reference, x is not quantised to 8-bit q8_1: each workgroup
  * stages it as 16-bit fixed point per 32-element block (x ~= s (256 hi +
  * lo), hi and lo int8, error <= amax/65278 per element); the weight quants
@@ -238,8 +255,11 @@ int cima_hip_attn_reduce(cima_hip_ctx* ctx, const float* part, void* out, int q_
  * counterpart in the reference: for callers that cannot allocate (HIP
  * graph capture, tight serving loops, harnesses that forbid it).  Limit:
  * q_heads * n_chunks * (dim + 2) * 4 bytes <= 4 MiB, else CIMA_E_INVALID.
- * Every call on a device shares that device's array: calls that overlap on
- * one device (other streams, other contexts) race. */
+ * The array belongs to the context: each context loads its own copy of
+ * the decode code object, so each holds its own 4 MiB of device memory
+ * until it is destroyed.  Calls on one context share that array and keep
+ * the last call's contents: calls on one context that overlap (on other
+ * streams) race; calls on different contexts do not. */
 int cima_hip_attn_decode_noalloc(cima_hip_ctx* ctx, const void* q, const void* k_cache, const void* v_cache,
                                  void* out, int q_heads, int kv_heads, int dim, int seq, int max_seq, int csz,
                                  int n_chunks, float scale, int window, const int* pos_dev);
@@ -410,6 +430,15 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
  * loads; *sink is written only in an improbable case.  The HBM read rate a
  * kernel can reach, measured the way the GEMVs are. */
 int cima_hip_stream_read(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink);
+/* The same read in a chosen form, for sweeping the read ceiling (no
+ * counterpart in the reference): dest 0 = into registers, `depth` loads of
+ * `width` bytes (16: depth 1, 2, 4, 8 or 16; 8: depth 4, 8 or 16) in flight
+ * per thread, grid-stride; dest 1 = into LDS through
+ * global_load_lds_dwordx4, a ring of `depth` (2, 4, 8, 16) 1 KB copies in
+ * flight per wave (width 16; whole 1 KB runs).  256-thread workgroups, at
+ * most wgs_per_cu (1..8) per CU. */
+int cima_hip_stream_read_cfg(cima_hip_ctx* ctx, const void* src, long long nbytes, unsigned int* sink, int dest,
+                             int depth, int width, int wgs_per_cu);
 
 #ifdef __cplusplus
 }

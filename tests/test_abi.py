@@ -250,3 +250,35 @@ def test_error_codes_match_header():
     codes = {name: int(v) for name, v in re.findall(r"#define CIMA_(E_[A-Z_]+)\s+(-?\d+)", text)}
     assert codes == {n: getattr(h, n) for n in codes}
     assert set(codes) == {"E_INVALID", "E_FORMAT", "E_NO_KERNEL", "E_NOT_INIT", "E_LIBRARY"}
+
+
+def test_x_range_flag_arithmetic():
+    """The prefill tiles' X range test (XRange in gguf_gemm.hip) is word
+    arithmetic on two bf16 halves at once; restated here in numpy and
+    checked over all 65536 x 2 half pairs' magnitudes against the
+    definition: overflow = |x| >= 65536 or not finite (f16 cannot hold it),
+    tiny = 0 < |x| < 2^-17 (f16 may drop its bits)."""
+    import numpy as np
+
+    h = np.arange(65536, dtype=np.uint32)
+    for lo_fixed in (0x0000, 0x3f80, 0x4780, 0x0001):
+        w = (h << 16) | lo_fixed
+        a = w & 0x7FFF7FFF
+        acc = ((a + 0x38803880) & 0x80008000) | ((~(a + 0x49004900) & (a + 0x7FFF7FFF) & 0x80008000) >> 1)
+        acc &= 0xFFFFFFFF
+        over = (acc & 0x80008000) != 0
+        tiny = (acc & 0x40004000) != 0
+
+        def ok(bits):
+            v = (bits.astype(np.uint32) << 16).view(np.float32)
+            return (~np.isfinite(v)) | (np.abs(v) >= 65536.0), (v != 0) & (np.abs(v) < 2.0 ** -17)
+
+        o_hi, t_hi = ok(h.astype(np.uint16))
+        o_lo, t_lo = ok(np.full(65536, lo_fixed, np.uint16))
+        assert np.array_equal(over, o_hi | o_lo)
+        assert np.array_equal(tiny, t_hi | t_lo)
+    # f32: bit 31 <- |x| >= 65520, the first value f16 rounds to inf
+    xs = np.array([65504.0, 65519.99, 65520.0, 1e9, np.inf, -70000.0, 1.0], np.float32)
+    f = ((xs.view(np.uint32) & 0x7FFFFFFF) + 0x38801000) & 0x80000000
+    assert list(f != 0) == [False, False, True, True, True, True, False]
+    assert np.isinf(np.float32(65520.0).astype(np.float16)) and not np.isinf(np.float32(65519.99).astype(np.float16))

@@ -211,8 +211,11 @@ def test_oracle_split_qkv_equals_fused():
 
 
 def test_sliding_window_metadata(tmp_path):
-    """A single sliding window in the metadata reaches the decoder config;
-    a per-layer window pattern is refused."""
+    """The reference's model_config (src/formats.rs:940-1007) ignores the
+    sliding-window key for qwen2 / llama files, so by default the loader
+    decodes with full attention (window 0) even when the file carries one;
+    with the opt-in, a single window reaches the decoder config and a
+    per-layer window pattern is refused."""
     from cima_amd.decoder import DecoderConfig, synthetic_model
 
     cfg = DecoderConfig(n_layers=1, hidden=256, q_heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=100,
@@ -221,8 +224,11 @@ def test_sliding_window_metadata(tmp_path):
     path = str(tmp_path / "win.gguf")
     gf.save_model(path, m)
     g = gf.GGUFFile(path)
-    assert gf.decoder_config(g).window == 96
+    assert gf.decoder_config(g).window == 0
+    assert gf.load_model(g).cfg.window == 0
+    assert gf.decoder_config(g, use_sliding_window=True).window == 96
     g.meta["qwen2.attention.sliding_window_pattern"] = 2
+    assert gf.decoder_config(g).window == 0
     with pytest.raises(gf.GGUFError):
-        gf.decoder_config(g)
+        gf.decoder_config(g, use_sliding_window=True)
     g.close()

@@ -57,21 +57,24 @@ def test_gemm_small_shapes(hip, t, m):
 
 @pytest.mark.parametrize("m", [16, 128, 512])
 def test_gemm_config4_full_shape(hip, m):
-    """Benchmark config 4: Q4_K W 14336x4096 x X (m tokens, bf16), Y fp32;
-    checked on a sample of 256 weight rows against the CPU path."""
+    """Benchmark config 4: Q4_K W 14336x4096 x X (m tokens, bf16), Y fp32,
+    every output row against the CPU path (the oracle's bit-exact f16 decode
+    of all of W, then the product in float64), so a wrong tile anywhere in
+    the row range fails; also per 128-row block, so one bad tile cannot hide
+    in the norm of the whole."""
     n, k = 14336, 4096
     w = synth.weights(Q4_K, 60, 0.02, n, k)
     xf = synth.normal(61, 1.0, m * k).reshape(m, k)
     y, xh = run(hip, Q4_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
-    rows = np.random.default_rng(m).choice(n, 256, replace=False)
-    rb = gguf.row_bytes(Q4_K, k)
-    wsub = np.stack([w[r] for r in rows])
-    w16 = oracle.dequant(Q4_K, wsub.reshape(-1), 256 * k)
-    want = oracle.gemm(xh, w16, m, 256, k)
-    r = rel(y[:, rows], want)
-    print(f"config 4 m={m}: rel err vs CPU path {r:.2e}")
+    assert gguf.row_bytes(Q4_K, k) == w.shape[1]
+    w16 = oracle.f16_bits_to_f32(oracle.dequant(Q4_K, w.reshape(-1), n * k)).reshape(n, k)
+    want = xh.astype(np.float64) @ w16.astype(np.float64).T
+    r = rel(y, want)
+    print(f"config 4 m={m}: rel err vs CPU path {r:.2e} over all {n} rows")
     assert r <= 1e-5
-    assert rb == w.shape[1]
+    for r0 in range(0, n, 128):
+        rb = rel(y[:, r0:r0 + 128], want[:, r0:r0 + 128])
+        assert rb <= 1e-5, (r0, rb)
 
 
 def test_gemm_tile_variants_agree(hip):
@@ -168,3 +171,45 @@ def test_gemm_narrow_weight_many_tokens(hip, n, k, m):
     y, xh = run(hip, Q4_K, w, xf, m, n, k, gguf.DT_BF16, gguf.DT_F32)
     want = oracle.gemm(xh, oracle.dequant(Q4_K, w, n * k), m, n, k)
     assert rel(y, want) <= 1e-5
+
+
+@pytest.mark.parametrize("m", [16, 64, 256], ids=["sk16", "reg_a", "lds_pipe"])
+def test_gemm_x_range_flags(hip, m):
+    """bf16 X beyond f16's range, or too small for it, no longer turns into
+    inf / zero silently: the tiles flag it (cima_hip_gemm_status) on every
+    tile kind, for the GGUF and the bitsandbytes weights; in-range bf16 and
+    any f16 X leave the word clear; f32 X flags only overflow."""
+    n, k = 256, 1024
+    w = torch.from_numpy(synth.weights(Q4_K, 70, 0.02, n, k)).cuda()
+    y = torch.empty((m, n), device="cuda")
+    hip.gemm_status(clear=True)
+
+    def flags(x, xd):
+        hip.gguf_gemm(Q4_K, x, w, y, m, n, k, n, xd, gguf.DT_F32)
+        return hip.gemm_status(clear=True)
+
+    base = torch.randn(m, k)
+    base[base.abs() < 1e-3] = 1e-3  # normal draws can land below 2^-17 themselves
+    assert flags(base.to(torch.bfloat16).cuda(), gguf.DT_BF16) == 0
+    assert flags(base.to(torch.float16).cuda(), gguf.DT_F16) == 0
+    assert flags(base.cuda(), gguf.DT_F32) == 0
+    big = base.clone()
+    big[m // 2, 777] = 70000.0
+    assert flags(big.to(torch.bfloat16).cuda(), gguf.DT_BF16) == 1
+    assert torch.isinf(y[m // 2]).any(), "the overflowing value reached the product as inf"
+    assert flags(big.cuda(), gguf.DT_F32) == 1
+    tiny = base.clone()
+    tiny[m - 1, 5] = 3e-7  # below 2^-17, nonzero
+    assert flags(tiny.to(torch.bfloat16).cuda(), gguf.DT_BF16) == 2
+    assert flags(tiny.cuda(), gguf.DT_F32) == 0
+    edge = base.clone()
+    edge[0, 0], edge[0, 1] = 65280.0, 2.0 ** -17  # the exact extremes
+    assert flags(edge.to(torch.bfloat16).cuda(), gguf.DT_BF16) == 0
+    # the bitsandbytes tiles report through the same word
+    from cima_amd import nf4
+    packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8).cuda()
+    absmax = torch.rand(n * k // 64).cuda() + 0.1
+    qmap = torch.from_numpy(nf4.NF4_CODE.copy()).cuda()
+    slab = torch.empty(2 * n * k, dtype=torch.uint8, device="cuda")
+    hip.nf4_gemm_slab(big.to(torch.bfloat16).cuda(), packed, absmax, qmap, y, m, n, k, 64, slab)
+    assert hip.gemm_status(clear=True) == 1

@@ -305,6 +305,36 @@ def test_gemv_deterministic(hip):
     assert np.array_equal(ys[0], ys[1]) and np.array_equal(ys[0], ys[2])
 
 
+@pytest.mark.parametrize("t, n, k", [(Q8_0, 14336, 4096), (Q8_0, 4864, 896), (Q4_K, 4096, 4096),
+                                     (Q6_K, 512, 14336), (Q4_0, 300, 2048)],
+                         ids=["q8_0-big", "q8_0-896", "q4_k", "q6_k-long", "q4_0"])
+@pytest.mark.parametrize("act", [gguf.DT_F16, gguf.DT_F32], ids=["f16", "f32"])
+def test_gemv_x_at_element_offset(hip, t, n, k, act):
+    """x, bias and y may sit at any element offset, as the reference's
+    pointers may (src/cuda.rs:2161): the result equals the aligned call's
+    bit for bit, with the residual epilogue, on every main loop the
+    heuristic picks for these shapes (the direct-to-LDS one for the large
+    Q8_0 matrix)."""
+    td = torch.float16 if act == gguf.DT_F16 else torch.float32
+    w = dev(synth.weights(t, seed=31, stddev=0.02, rows=n, k=k))
+    xv = torch.from_numpy(synth.normal(32, 1.0, k)).to(td).cuda()
+    bv = torch.from_numpy(synth.normal(33, 0.1, n)).to(td).cuda()
+    y0v = torch.from_numpy(synth.normal(34, 1.0, n)).to(td).cuda()
+    ya = y0v.clone()
+    hip.gguf_gemv(t, xv, w, bv, ya, n, k, 1, act)
+    for off in (1, 3):
+        xb = torch.zeros(k + 8, dtype=td, device="cuda")
+        bb = torch.zeros(n + 8, dtype=td, device="cuda")
+        yb = torch.zeros(n + 8, dtype=td, device="cuda")
+        xb[off:off + k] = xv
+        bb[off:off + n] = bv
+        yb[off:off + n] = y0v
+        hip.gguf_gemv(t, xb[off:off + k], w, bb[off:off + n], yb[off:off + n], n, k, 1, act)
+        torch.cuda.synchronize()
+        assert torch.equal(yb[off:off + n], ya), off
+        assert not yb[:off].any() and not yb[off + n:].any()
+
+
 def test_gemv_argument_errors(hip):
     x = torch.zeros(256, dtype=torch.float32, device="cuda")
     w = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
@@ -320,7 +350,7 @@ def test_gemv_argument_errors(hip):
         hip.gguf_gemv(10, x, w, None, y, 4, 256, 0)  # Q2_K: not a format the reference executes
     assert e.value.code == E_FORMAT
     with pytest.raises(EngineError) as e:
-        hip.gguf_gemv(Q4_K, x.data_ptr() + 4, w, None, y, 1, 128 * 2, 0)  # x not 16-B aligned
+        hip.gguf_gemv(Q4_K, x.data_ptr() + 2, w, None, y, 1, 128 * 2, 0)  # f32 x not 4-B aligned
     assert e.value.code == E_INVALID
     with pytest.raises(EngineError) as e:
         hip.gguf_gemv(Q4_K, x, w.data_ptr() + 2, None, y, 1, 256, 0)  # Q4_K weights need 16 B
