@@ -82,7 +82,7 @@ const int kFormats[] = {CIMA_GGML_Q8_0, CIMA_GGML_Q4_0, CIMA_GGML_Q4_1, CIMA_GGM
 const int kGemmBN[] = {16, 32, 64, 128, 256};
 
 // (lanes per row, unit steps) of the direct-to-LDS streaming GEMVs built
-const int kDmaShapes[][2] = {{64, 1}, {64, 2}, {32, 1}, {16, 1}};
+const int kDmaShapes[][2] = {{64, 1}, {64, 2}, {32, 1}, {32, 2}, {16, 1}};
 
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
@@ -119,6 +119,7 @@ struct cima_hip_ctx {
     int tune_ring = 0;     // GEMV main loop: 0 = heuristic, 1 = item ring where built, 2 = never
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_dma = 0;      // direct-to-LDS streaming GEMV: 0 = heuristic, 1 = wherever built, 2 = never
+    int tune_ksplit = 0;   // 16-token GEMM k-split with a slab: 0 = heuristic, 1 = never, 2/4/8 = that many
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
     // this device's copy of the decode code object's `scratch` array
@@ -259,8 +260,8 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
 }
 
 // Direct-to-LDS streaming GEMV (the _dma kernels, RING == 3 in
-// gguf_gemv.hip).  Built for lanes per row 64 with 1 or 2 units per lane and
-// step, and 32 or 16 with 1.  An item is a segment of lpr * iters units of
+// gguf_gemv.hip).  Built for lanes per row 64 or 32 with 1 or 2 units per
+// lane and step, and 16 with 1.  An item is a segment of lpr * iters units of
 // each of the wave's 64 / lpr rows and each weight stream; its LDS slot
 // holds, per row segment, the 16-byte lines that cover it, in whole 1 KB
 // copies.  These sizes match the kernel's SEGB / NPC / NCH / SLOT.
@@ -268,12 +269,13 @@ struct DmaPlan {
     int lpr, iters;
     unsigned slot;  // LDS bytes per item
 };
-DmaPlan plan_dma(const Fmt* F, int k, bool pair) {
+DmaPlan plan_dma(const Fmt* F, int k, bool pair, int lpr_override) {
     const int units = k / F->gemv_unit;
     int lpr = pow2_ceil(units);
     if (lpr < 16) lpr = 16;
     if (lpr > 64) lpr = 64;
-    const int iters = (lpr == 64 && units > 64) ? 2 : 1;
+    if (lpr_override == 16 || lpr_override == 32 || lpr_override == 64) lpr = lpr_override;
+    const int iters = (lpr >= 32 && units > lpr) ? 2 : 1;
     const int segb = lpr * iters * F->gemv_unit / F->block_elems * F->block_bytes;
     const int npc = (segb + 30) / 16;
     const int nch = (npc + 63) / 64;
@@ -335,19 +337,24 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     // Direct-to-LDS streaming.  Measured on MI355X (cold weights, us):
     // Q8_0 14336x4096 15.4 -> 13.3 (one item in flight per wave, three
     // workgroups per CU), the Q8_0 gate+up pair 29.8 -> 23.4 (two items in
-    // flight); slower than the register loops for Q4_K (14336x4096 8.2 ->
-    // 9.4), for rows of several segments (4096x14336: Q8_0 17.2 -> 19.1,
-    // Q4_K 9.9 -> 12.3) and for matrices of a few MB (about 1 us more), so
-    // the heuristic takes it for large Q8_0 matrices of one-segment rows.
+    // flight), the Q8_0 151936x896 head 35.0 -> 27.0 (items of two 952-byte
+    // rows: two in flight, four workgroups per CU); slower than the
+    // register loops for Q4_K (14336x4096 8.2 -> 9.4), for rows of several
+    // segments (4096x14336: Q8_0 17.2 -> 19.1, Q4_K 9.9 -> 12.3) and for
+    // matrices of a few MB (about 1 us more), so the heuristic takes it for
+    // large Q8_0 matrices of one-segment rows.
     bool dma = false;
-    int depth = 1;
-    const DmaPlan dplan = plan_dma(F, k, pair);
+    int depth = 1, dma_wgs = 3;
+    const DmaPlan dplan = plan_dma(F, k, pair, ctx->tune_dma != 0 ? ctx->tune_lpr : 0);
     const bool one_seg = k / F->gemv_unit <= dplan.lpr * dplan.iters;
     const double wbytes_all = (pair ? 2.0 : 1.0) * (double)n * (double)(k / F->block_elems) * F->block_bytes;
     const bool dma_auto = t == CIMA_GGML_Q8_0 && one_seg && wbytes_all >= 24e6 && kind != GK_ATT;
-    if (ctx->tune_dma != 2 && !(ctx->tune_rows > 1) && !ctx->tune_lpr && (ctx->tune_dma != 0 || dma_auto)) {
+    if (ctx->tune_dma != 2 && !(ctx->tune_rows > 1) && (!ctx->tune_lpr || ctx->tune_dma != 0) &&
+        (ctx->tune_dma != 0 || dma_auto)) {
         const DmaPlan d = dplan;
-        depth = ctx->tune_dma == 3 || (ctx->tune_dma == 0 && pair) ? 2 : 1;
+        const bool small_items = d.slot / (pair ? 2 : 1) < 3072;
+        depth = ctx->tune_dma == 3 || (ctx->tune_dma == 0 && (pair || small_items)) ? 2 : 1;
+        dma_wgs = small_items ? 4 : 3;
         const unsigned xb = (unsigned)((gemv_lds_bytes(F, k) + 15) & ~(size_t)15) + (kind == GK_ATT ? 4u * (unsigned)k : 0u);
         const unsigned lds = xb + (unsigned)(kGemvThreads / 64) * depth * d.slot;
         if ((long)lds <= ctx->max_lds) {
@@ -383,7 +390,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     // persistent grid: one workgroup per CU for the item ring and for Q8_0,
     // two otherwise (measured on MI355X)
     const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs
-                                       : (dma ? 3 : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2));
+                                       : (dma ? dma_wgs : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2));
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;
@@ -530,6 +537,8 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                         if (!rc) rc = add(MOD_GEMM, name);
                     }
                 }
+    if (!rc) rc = add(MOD_GEMM, "cima_gemm_ksum_f32");
+    if (!rc) rc = add(MOD_GEMM, "cima_gemm_ksum_f16");
     if (!rc) rc = add(MOD_DEQUANT, "cima_stream_read");
     for (const char* kn : {"cima_stream_read_r1_w16", "cima_stream_read_r2_w16", "cima_stream_read_r4_w16",
                            "cima_stream_read_r8_w16", "cima_stream_read_r16_w16", "cima_stream_read_r4_w8",
@@ -567,6 +576,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_RINGL")) ctx->tune_ringl = atoi(s);
     if (const char* s = getenv("CIMA_GEMV_DMA")) ctx->tune_dma = atoi(s);
     if (const char* s = getenv("CIMA_GEMM_XCHECK")) ctx->gemm_xcheck = atoi(s) != 0;
+    if (const char* s = getenv("CIMA_GEMM_KSPLIT")) ctx->tune_ksplit = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -783,13 +793,39 @@ struct GemmExt {
     long long bsz;
     int bs_shift;
     unsigned* status;
+    float* part;
+    int ksplit;
 };
 
 // Launches cima_gemm_<fname>_b<BN>[n]_<x>_<y> over Y[m, n] (row stride ldy):
 // the token tile from fused_bn (or the tuning override), 16-token tiles
 // only for k % 128 == 0.
+// Workgroups along k for the 16-token tiles (1 = none), when the caller's
+// slab can hold the partial tiles (S x m x n fp32) and the 128-k stages
+// divide evenly (at least four per split, one per k-split wave).  A grid
+// of 32-row tiles of at most one workgroup per CU is split two ways, a grid
+// of 16-row tiles (the narrow kernels, three or four per CU) four ways at
+// most a quarter workgroup per CU and two ways at most a half.  Measured
+// on MI355X (Q4_K unless noted, bf16 X, cold, us, unsplit -> split): 32
+// tokens: 4096x14336 43.6 -> 30.1 (Q8_0 64.5 -> 48.5), 1024x4096 9.6 ->
+// 8.9, 4096x4096 13.2 -> 13.3; 16 tokens: 6144x4096 15.5 -> 13.9,
+// 1024x4096 9.5 -> 7.9; splitting fuller grids loses (16 tokens:
+// 4096x14336 26.4 -> 27.7, 4096x4096 9.8 -> 12.2, 14336x4096 19.0 -> 23.4).
+int pick_ksplit(const cima_hip_ctx* ctx, int wgs, bool narrow, int m, int n, int k, size_t part_bytes) {
+    const int stages = k / 128;
+    auto fits = [&](int s) { return stages % s == 0 && stages / s >= 4 && (size_t)s * m * n * 4 <= part_bytes; };
+    if (ctx->tune_ksplit == 1) return 1;
+    if (ctx->tune_ksplit > 1) return fits(ctx->tune_ksplit) ? ctx->tune_ksplit : 1;
+    int s = 1;
+    if (!narrow) s = wgs <= ctx->num_cu ? 2 : 1;
+    else s = 4 * wgs <= ctx->num_cu ? 4 : (2 * wgs <= ctx->num_cu ? 2 : 1);
+    while (s > 1 && !fits(s)) s /= 2;
+    return s;
+}
+
 int gemm_launch(cima_hip_ctx* ctx, const char* fname, const void* x, const void* w, void* y, int m, int n, int k,
-                int ldy, int x_dtype, int y_dtype, const GemmExt& gext, const char* api) {
+                int ldy, int x_dtype, int y_dtype, const GemmExt& gext, const char* api, float* part = nullptr,
+                size_t part_bytes = 0) {
     // the 16-token tile stages 128 k at a time (32-row weight tiles in
     // 512-thread workgroups), so it needs k % 128 == 0
     int bn = fused_bn(m, n, ctx->num_cu);
@@ -816,11 +852,23 @@ int gemm_launch(cima_hip_ctx* ctx, const char* fname, const void* x, const void*
     int mm = m, nn = n, kk = k, ld = ldy;
     GemmExt ge = gext;
     ge.status = ctx->gemm_xcheck ? ctx->gemm_status : nullptr;
+    const unsigned gx = (unsigned)((n + bm - 1) / bm), gy = (unsigned)((m + bn - 1) / bn);
+    const int ks = bn == 16 && part ? pick_ksplit(ctx, (int)(gx * gy), narrow, m, n, k, part_bytes) : 1;
+    ge.part = ks > 1 ? part : nullptr;
+    ge.ksplit = ks;
     void* args[] = {&xa, &wa, &ya, &mm, &nn, &kk, &ld, &ge};
     const unsigned threads = bn == 16 && !narrow ? 512 : 256;
-    hipError_t e = hipModuleLaunchKernel(f, (unsigned)((n + bm - 1) / bm), (unsigned)((m + bn - 1) / bn), 1, threads, 1,
-                                         1, 0, ctx->stream, args, nullptr);
-    return e == hipSuccess ? 0 : hip_fail(e, api);
+    hipError_t e = hipModuleLaunchKernel(f, gx, gy, (unsigned)ks, threads, 1, 1, 0, ctx->stream, args, nullptr);
+    if (e != hipSuccess) return hip_fail(e, api);
+    if (ks == 1) return 0;
+    // the partial tiles, summed in a fixed order into Y
+    hipFunction_t fs;
+    if (int rc = get_fn(ctx, y_dtype == CIMA_DT_F32 ? "cima_gemm_ksum_f32" : "cima_gemm_ksum_f16", &fs)) return rc;
+    const float* pa = part;
+    int S = ks;
+    void* sargs[] = {&pa, &ya, &mm, &nn, &ld, &S};
+    const long long outs = (long long)m * n;
+    return launch(ctx, fs, (unsigned)((outs + 255) / 256), 256, sargs, api);
 }
 int gemm_fused(cima_hip_ctx* ctx, const Fmt* F, const void* x, const void* w, void* y, int m, int n, int k, int ldy,
                int x_dtype, int y_dtype, const char* api) {
@@ -853,8 +901,10 @@ int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int t, const void* x, const void*
     if (rc || !F) return rc;
     if (slab_bytes && (!slab || !aligned(slab, 256)))
         return fail(CIMA_E_INVALID, "%s: slab must be a non-null 256-byte aligned device pointer", api);
-    // the fused kernels dequantise W tile by tile: the slab is not needed
-    return gemm_fused(ctx, F, x, w, y, m, n, k, ldy, x_dtype, y_dtype, api);
+    // the fused kernels dequantise W tile by tile; the slab holds the
+    // partial tiles when a narrow weight is split along k at 16 tokens
+    return gemm_launch(ctx, F->name, x, w, y, m, n, k, ldy, x_dtype, y_dtype, GemmExt{}, api,
+                       slab_bytes ? static_cast<float*>(slab) : nullptr, (size_t)slab_bytes);
 }
 
 
@@ -1431,7 +1481,7 @@ int cima_hip_nf4_gemm_slab(cima_hip_ctx* ctx, const void* x, const void* packed,
     if (k % 64 == 0 && blocksize % 32 == 0 && aligned(packed, 16) && aligned(absmax, 4)) {
         const int sh = (blocksize & (blocksize - 1)) == 0 ? log2i(blocksize) : -1;
         return gemm_launch(ctx, "nf4", x, packed, y, m, n, k, n, x_dtype, y_dtype,
-                           GemmExt{absmax, qmap, (long long)blocksize, sh, nullptr}, api);
+                           GemmExt{absmax, qmap, (long long)blocksize, sh, nullptr, nullptr, 1}, api);
     }
     // Slab route for the other shapes: W is decoded into the slab a row
     // slice at a time (the reference's lin_gemm works through its 32 MiB

@@ -212,6 +212,8 @@ struct GemmExt {
     long long bsz;   // elements per absmax entry
     int bs_shift;    // log2(bsz) when bsz is a power of two, else -1
     unsigned* status;  // X range flags (cima_gemm_status), OR-ed in
+    float* part;       // k-split partial tiles, [ksplit][m][n] fp32 (16-token tiles only)
+    int ksplit;        // workgroups along k (blockIdx.z); 1 = Y written directly
 };
 
 // X range report.  The tiles round X to f16.  That is exact for bf16 values
@@ -272,9 +274,9 @@ struct XScan {
         if constexpr (XT != XT_F16) {
             if (!on) return;
             const long long nw = (long long)m * k * (XT == XT_F32 ? 4 : 2) / 16;
-            const long long nwg = (long long)gridDim.x * gridDim.y;
+            const long long nwg = (long long)gridDim.x * gridDim.y * gridDim.z;
             const long long per = (nw + nwg - 1) / nwg;
-            w0 = ((long long)blockIdx.y * gridDim.x + blockIdx.x) * per;
+            w0 = (((long long)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * per;
             we = min(w0 + per, nw);
             const uint4* p = static_cast<const uint4*>(x);
             // Loads in asm: compiled as plain loads, predicated per lane,
@@ -683,7 +685,11 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
     const auto dc = D::ctx(w, ext);
     fmt_init<D>(dc, ext);
     XScan<XT, 64 * NW> xscan;
-    const int nk = k / 128, cnt = (nk + 3) >> 2;  // every wave runs cnt steps (a uniform barrier count)
+    // k-split over workgroups (blockIdx.z of ext.ksplit; the host makes the
+    // 128-k stages divide evenly): this workgroup's stages [s0, s0 + nk)
+    const int ksp = ext.ksplit > 1 ? ext.ksplit : 1;
+    const int nk = k / 128 / ksp, s0 = (int)blockIdx.z * nk;
+    const int cnt = (nk + 3) >> 2;  // every wave runs cnt steps (a uniform barrier count)
     const uint8_t* wp = w + (size_t)min(r0 + 16 * rt + (lane & 15), n - 1) * row_bytes;
     // this lane's share of the split's x tile: E elements of one token
     const int lt = 64 * rt + lane, xtok = (lt * E) >> 7, xk = (lt * E) & 127;
@@ -693,7 +699,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
         uint4 xr[XW];
     };
     auto issue = [&](Stage& st, int i) {
-        const int s = min(ks + 4 * i, nk - 1);  // past the split's last stage: re-load the last one
+        const int s = s0 + min(ks + 4 * i, nk - 1);  // past the split's last stage: re-load the last one
         st.wr = D::load(dc, wp, 4 * s + g);
 #pragma unroll
         for (int j = 0; j < XW; j++) st.xr[j] = reinterpret_cast<const uint4*>(xp + (size_t)s * 128 * ES)[j];
@@ -730,7 +736,7 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
             }
         }
         uint32_t o[16];
-        D::deq(dc, st.wr, 4 * min(ks + 4 * i, nk - 1) + g, o);
+        D::deq(dc, st.wr, 4 * (s0 + min(ks + 4 * i, nk - 1)) + g, o);
         __syncthreads();
         if (next) issue(st, i + PF);
         __builtin_amdgcn_sched_barrier(0);
@@ -767,9 +773,13 @@ __device__ void gemm_body_sk16(const void* __restrict__ x, const uint8_t* __rest
                         (red[(2 * RT + ot) * 256 + oi] + red[(3 * RT + ot) * 256 + oi]);
         const int row = r0 + orow, tok = t0 + otok;
         if (row < n && tok < m) {
-            const size_t off = (size_t)tok * ldy + row;
-            if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = v;
-            else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(v);
+            if (ksp > 1) {
+                ext.part[((size_t)blockIdx.z * m + tok) * n + row] = v;  // summed by cima_gemm_ksum_*
+            } else {
+                const size_t off = (size_t)tok * ldy + row;
+                if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = v;
+                else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(v);
+            }
         }
     }
 
@@ -1003,3 +1013,27 @@ GEMM_SMALL(XT_BF16, bf16, XT_F32, f32)
 GEMM_SMALL(XT_F32, f32, XT_F16, f16)
 GEMM_SMALL(XT_F16, f16, XT_F16, f16)
 GEMM_SMALL(XT_BF16, bf16, XT_F16, f16)
+
+
+// Y[tok, row] (row stride ldy) = sum over z < S of part[z][tok][row], z in
+// order: the k-split partial tiles of the 16-token kernels, added in one
+// fixed order (results do not depend on the launch)
+template <int YT>
+__device__ void ksum_body(const float* __restrict__ part, void* __restrict__ y, int m, int n, int ldy, int S) {
+    const long long o = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (o >= (long long)m * n) return;
+    const int tok = (int)(o / n), row = (int)(o % n);
+    float v = part[o];
+    for (int z = 1; z < S; z++) v += part[(size_t)z * m * n + o];
+    const size_t off = (size_t)tok * ldy + row;
+    if constexpr (YT == XT_F32) static_cast<float*>(y)[off] = v;
+    else static_cast<uint16_t*>(y)[off] = (uint16_t)f2h(v);
+}
+extern "C" __global__ __launch_bounds__(256) void cima_gemm_ksum_f32(const float* part, void* y, int m, int n, int ldy,
+                                                                     int S) {
+    ksum_body<XT_F32>(part, y, m, n, ldy, S);
+}
+extern "C" __global__ __launch_bounds__(256) void cima_gemm_ksum_f16(const float* part, void* y, int m, int n, int ldy,
+                                                                     int S) {
+    ksum_body<XT_F16>(part, y, m, n, ldy, S);
+}

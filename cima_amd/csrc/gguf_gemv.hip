@@ -1444,7 +1444,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #define GEMV_DMA_SHAPE(FN, F, L, LS, IT) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 1) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 2)
 #define GEMV_DMA(FN, F)                                                                                 \
     GEMV_DMA_SHAPE(FN, F, 64, 6, 1) GEMV_DMA_SHAPE(FN, F, 64, 6, 2) GEMV_DMA_SHAPE(FN, F, 32, 5, 1)       \
-    GEMV_DMA_SHAPE(FN, F, 16, 4, 1)
+    GEMV_DMA_SHAPE(FN, F, 32, 5, 2) GEMV_DMA_SHAPE(FN, F, 16, 4, 1)
 
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \

@@ -103,8 +103,9 @@ int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
  * heuristic, 1 = the direct-to-LDS streaming kernels with one item in flight
  * per wave wherever they are built and fit, 3 = the same with two, 2 =
  * never them (the register-ring kernels).  Environment variable
- * CIMA_GEMV_DMA at init.  A set_gemv_tuning override of rows or lanes also
- * selects the register kernels. */
+ * CIMA_GEMV_DMA at init.  A set_gemv_tuning override of rows selects the
+ * register kernels; one of lanes does too under the heuristic (mode 0) and
+ * picks the streaming kernels' lanes per row (16, 32 or 64) under 1 or 3. */
 int cima_hip_set_gemv_dma(cima_hip_ctx* ctx, int mode);
 
 /* GEMV grid tuning (no counterpart in the reference): the persistent grid
@@ -184,10 +185,11 @@ int cima_hip_gguf_gemv_swiglu(cima_hip_ctx* ctx, int ggml_type, const void* x,
  * W tile, bit-exact f16, into LDS (128-token tiles) or straight into the
  * MFMA operand registers (up to 64 tokens), and multiplies with f16 MFMA,
  * fp32 accumulate.  x_dtype: CIMA_DT_F32, CIMA_DT_F16 or CIMA_DT_BF16,
- * converted to f16 -- exact for 2^-14 <= |x| < 65520; beyond, values
- * overflow to +-inf and below lose bits as f16 subnormals, with no error
- * (the engine's activations are f16 already, saturated to +-65000 by its
- * RMSNorm, so nothing is lost there); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
+ * converted to f16 -- exact for bf16 of 2^-17 <= |x| < 65536; beyond,
+ * values overflow to +-inf and below may lose bits as f16 subnormals, which
+ * the call reports through cima_hip_gemm_status (the engine's activations
+ * are f16 already, saturated to +-65000 by its RMSNorm, so nothing is lost
+ * there); y_dtype: CIMA_DT_F32 or CIMA_DT_F16.
  * Requires k % 64 == 0 (and k % 256 for K-quants), x 16-byte aligned. */
 int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                        int m, int n, int k, int ldy, int x_dtype, int y_dtype);
@@ -197,8 +199,13 @@ int cima_hip_gguf_gemm(cima_hip_ctx* ctx, int ggml_type, const void* x, const vo
  * 618-655, src/quant.rs:120-129), whose gguf_dequant into the DQ_SCRATCH
  * slab + gemm_dispatch (src/cuda.rs:2285-2320, 2468-2541) runs here as the
  * fused MFMA kernels of cima_hip_gguf_gemm: W is dequantised tile by tile
- * and never expanded, so the slab (256-byte aligned when given) is not
- * touched and any size, 0 included, works.  No library GEMM is involved. */
+ * and never expanded, and any slab size, 0 included, works.  No library
+ * GEMM is involved.  At up to 32 tokens a weight too narrow to fill the
+ * CUs is split along k over more workgroups, with the S partial tiles
+ * (S x m x n fp32, S = 2 or 4) in the slab (256-byte aligned) and summed
+ * into Y in a fixed order by a second launch; without room in the slab
+ * the call runs unsplit.  The slab's contents are then scratch: calls that
+ * share a slab must not overlap. */
 int cima_hip_gguf_gemm_slab(cima_hip_ctx* ctx, int ggml_type, const void* x, const void* w, void* y,
                             int m, int n, int k, int ldy, int x_dtype, int y_dtype, void* slab,
                             unsigned long long slab_bytes);

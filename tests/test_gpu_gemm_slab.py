@@ -3,7 +3,8 @@
 transformer.rs:618-655) decodes W into an f16 slab with gguf_dequant and
 multiplies it with cublasGemmEx (src/cuda.rs:2468-2541); here the same
 call runs the fused MFMA kernels, which dequantise W bit-exactly tile by
-tile, so the slab is never touched and no library GEMM runs.  Checked
+tile, so W is never expanded and no library GEMM runs; the slab only holds
+the partial tiles of narrow weights split along k at up to 32 tokens.  Checked
 against the CPU path (f16 dequant + fp64 GEMM of the f16-rounded X): 1e-5
 with fp32 Y, where only the summation order differs, and the north star's
 1e-3 with f16 Y."""
@@ -123,4 +124,59 @@ def test_slab_entry_graph_replay(hip):
         torch.cuda.synchronize()
         assert np.array_equal(yg.cpu().numpy(), eager), i
         hip.gguf_gemm_slab(Q4_K, x, w, y, m, n, k, slab)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("t, n, k, m", [(Q4_K, 4096, 14336, 16), (Q4_K, 4096, 14336, 32), (Q8_0, 4096, 14336, 32),
+                                        (Q4_K, 1024, 4096, 16), (Q4_K, 1024, 4096, 32), (Q4_K, 6144, 4096, 16),
+                                        (Q6_K, 1024, 4096, 20)],
+                         ids=["q4k-down-m16", "q4k-down-m32", "q8-down-m32", "q4k-kv-m16", "q4k-kv-m32",
+                              "q4k-qkv-m16", "q6k-kv-m20"])
+def test_slab_entry_k_split(hip, t, n, k, m):
+    """Narrow weights at up to 32 tokens split along k over more workgroups,
+    with the partial tiles in the caller's slab and a fixed-order sum (the
+    long-row down projection at 32 tokens among them): every output row
+    against the CPU path (1e-5), against the unsplit product (1e-6: only
+    the order of the k sum differs), bit-identical run to run and in a
+    replayed graph; a slab too small for the partials runs unsplit, giving
+    cima_hip_gguf_gemm's bits."""
+    w = synth.weights(t, 130, 0.02, n, k)
+    wd = torch.from_numpy(w).cuda()
+    x = torch.from_numpy(synth.normal(131 + m, 1.0, m * k).reshape(m, k)).to(torch.bfloat16).cuda()
+    slab = torch.empty(32 << 20, dtype=torch.uint8, device="cuda")
+    y1 = torch.empty((m, n), device="cuda")
+    y2 = torch.empty((m, n), device="cuda")
+    yu = torch.empty((m, n), device="cuda")
+    hip.gguf_gemm_slab(t, x, wd, y1, m, n, k, slab)
+    hip.gguf_gemm_slab(t, x, wd, y2, m, n, k, slab)
+    hip.gguf_gemm(t, x, wd, yu, m, n, k)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    got, unsplit = y1.cpu().numpy(), yu.cpu().numpy()
+    assert rel(got, unsplit) <= 1e-6
+    w16 = oracle.f16_bits_to_f32(oracle.dequant(t, w, n * k)).reshape(n, k)
+    xh = x.float().cpu().numpy().astype(np.float64)
+    assert rel(got, xh @ w16.astype(np.float64).T) <= 1e-5
+    tiny = torch.empty(1024, dtype=torch.uint8, device="cuda")
+    ys = torch.empty((m, n), device="cuda")
+    hip.gguf_gemm_slab(t, x, wd, ys, m, n, k, tiny)
+    torch.cuda.synchronize()
+    assert torch.equal(ys, yu)
+    # captured and replayed, eager work between replays
+    g = torch.cuda.CUDAGraph()
+    yg = torch.zeros((m, n), device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            hip.set_stream(s.cuda_stream)
+            hip.gguf_gemm_slab(t, x, wd, yg, m, n, k, slab)
+    hip.use_torch_stream()
+    torch.cuda.synchronize()
+    for i in range(3):
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(yg, y1), i
+        hip.gguf_gemm_slab(t, x, wd, y2, m, n, k, slab)
         torch.cuda.synchronize()
