@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--calib", action="store_true",
                     help="also run a 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--leg", choices=["q8_0_14336x4096", "q8_0_pair", "q8_0_head_151936x896"], default=None,
+                    help="run only this GEMV --steps times on cycled cold copies (and --calib), for counter "
+                         "passes of rocprofv3; prints nothing")
     return ap.parse_args()
 
 
@@ -147,6 +150,31 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.leg:
+        # one GEMV shape alone, for per-dispatch counters (FETCH_SIZE /
+        # WRITE_SIZE): Q8_0 at Llama-3-8B gate/up, the Q8_0 gate+up pair,
+        # or the Qwen2.5-0.5B Q8_0 tied head with its argmax (f16 x)
+        n, k = (151936, 896) if args.leg == "q8_0_head_151936x896" else (FFN, HID)
+        pair = args.leg == "q8_0_pair"
+        copies = [torch.from_numpy(synth.weights(Q8_0, 400 + i, 0.02, n, k)).to(dev) for i in range(2 if pair else 1)]
+        copies = [c.clone() for c in copies for _ in range(6)]
+        if args.leg == "q8_0_head_151936x896":
+            xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev).half()
+            ys = torch.empty(n, device=dev, dtype=torch.float16)
+            slot = torch.zeros(1, dtype=torch.int64, device=dev)
+        else:
+            xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev)
+            ys = torch.empty(n, device=dev)
+        for i in range(args.steps):
+            if pair:
+                ctx.gguf_gemv_swiglu(Q8_0, xs, copies[(2 * i) % len(copies)], copies[(2 * i + 1) % len(copies)],
+                                     None, None, ys, n, k)
+            elif args.leg == "q8_0_head_151936x896":
+                ctx.gguf_gemv_argmax(Q8_0, xs, None, 0.0, copies[i % len(copies)], ys, n, k, slot)
+            else:
+                ctx.gguf_gemv(Q8_0, xs, copies[i % len(copies)], None, ys, n, k, 0)
+        torch.cuda.synchronize()
+        return
 
     # eager pass first (loads kernels, checks arguments)
     for L in layers[:2]:

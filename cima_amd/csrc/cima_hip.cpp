@@ -267,6 +267,7 @@ GemvPlan plan_gemv(const cima_hip_ctx* ctx, const Fmt* F, int n, int k, bool pai
 // copies.  These sizes match the kernel's SEGB / NPC / NCH / SLOT.
 struct DmaPlan {
     int lpr, iters;
+    int segb;       // bytes of one row segment
     unsigned slot;  // LDS bytes per item
 };
 DmaPlan plan_dma(const Fmt* F, int k, bool pair, int lpr_override) {
@@ -280,7 +281,7 @@ DmaPlan plan_dma(const Fmt* F, int k, bool pair, int lpr_override) {
     const int npc = (segb + 30) / 16;
     const int nch = (npc + 63) / 64;
     const unsigned slot = (unsigned)((pair ? 2 : 1) * (64 / lpr) * nch * 1024);
-    return DmaPlan{lpr, iters, slot};
+    return DmaPlan{lpr, iters, segb, slot};
 }
 
 int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const void* wb,
@@ -352,7 +353,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     if (ctx->tune_dma != 2 && !(ctx->tune_rows > 1) && (!ctx->tune_lpr || ctx->tune_dma != 0) &&
         (ctx->tune_dma != 0 || dma_auto)) {
         const DmaPlan d = dplan;
-        const bool small_items = d.slot / (pair ? 2 : 1) < 3072;
+        const bool small_items = d.segb <= 1536;  // rows of at most ~1.5 KB (k = 896 at Q8_0: 952 B)
         depth = ctx->tune_dma == 3 || (ctx->tune_dma == 0 && (pair || small_items)) ? 2 : 1;
         dma_wgs = small_items ? 4 : 3;
         const unsigned xb = (unsigned)((gemv_lds_bytes(F, k) + 15) & ~(size_t)15) + (kind == GK_ATT ? 4u * (unsigned)k : 0u);
