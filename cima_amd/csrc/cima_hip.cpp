@@ -83,6 +83,11 @@ const int kGemmBN[] = {16, 32, 64, 128, 256};
 
 // (lanes per row, unit steps) of the direct-to-LDS streaming GEMVs built
 const int kDmaShapes[][2] = {{64, 1}, {64, 2}, {32, 1}, {32, 2}, {16, 1}};
+// which depths are built: one item in flight everywhere; two for the
+// gate+up pair and for the short-row shapes (one unit at 16 or 32 lanes)
+bool dma_built(int lpr, int iters, int depth, bool pair) {
+    return depth == 1 || pair || (iters == 1 && lpr <= 32);
+}
 
 // (rows, unit steps) pairs the code object is built for (R * ITERS <= 8)
 const int kShapes[][2] = {{1, 1}, {1, 2}, {1, 4}, {1, 8}, {2, 1}, {2, 2}, {2, 4}};
@@ -120,6 +125,7 @@ struct cima_hip_ctx {
     int tune_ringl = 0;    // stepped ring: 0 = heuristic (8 units per lane), 1 = from 2 units per lane, 2 = never
     int tune_dma = 0;      // direct-to-LDS streaming GEMV: 0 = heuristic, 1 = wherever built, 2 = never
     int tune_ksplit = 0;   // 16-token GEMM k-split with a slab: 0 = heuristic, 1 = never, 2/4/8 = that many
+    int tune_wsplit = 0;   // GEMV rows split over the workgroup's waves: 0 = heuristic, 1 = always, 2 = never
     int tune_nf4_rows = 0;  // NF4 GEMV rows per wave (0 = heuristic, else 1, 2 or 4)
     int tune_nf4_kernel = 0;  // NF4 GEMV: 0 = heuristic, 1 = LDS pair table, 2 = register codebook
     // this device's copy of the decode code object's `scratch` array
@@ -355,6 +361,7 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
         const DmaPlan d = dplan;
         const bool small_items = d.segb <= 1536;  // rows of at most ~1.5 KB (k = 896 at Q8_0: 952 B)
         depth = ctx->tune_dma == 3 || (ctx->tune_dma == 0 && (pair || small_items)) ? 2 : 1;
+        if (!dma_built(d.lpr, d.iters, depth, pair)) depth = 1;
         dma_wgs = small_items ? 4 : 3;
         const unsigned xb = (unsigned)((gemv_lds_bytes(F, k) + 15) & ~(size_t)15) + (kind == GK_ATT ? 4u * (unsigned)k : 0u);
         const unsigned lds = xb + (unsigned)(kGemvThreads / 64) * depth * d.slot;
@@ -368,9 +375,30 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
             p.ring = p.ringl = false;
         }
     }
+    // Rows split over the workgroup's four waves (the _ksplit kernels):
+    // long rows, each wave a quarter of every row with its x fragment in
+    // registers, for plain and epilogue GEMVs
+    const int units_all = k / F->gemv_unit;
+    const int wq = (units_all + 3) / 4;  // units per wave
+    const bool wsplit_ok = !dma && !pair && kind == GK_PLAIN && wq <= 128 && units_all > 128 && !(ctx->tune_rows > 1);
+    // measured on MI355X (cold, us, 4096x14336, fp32 x): Q6_K 16.9 -> 15.1;
+    // slower for Q4_K (9.9 -> 11.5), Q8_0 (18.5 -> 19.3), Q4_0 (12.7 ->
+    // 13.6) and the decode step's Q8_0 896x4864 (3.7 -> 5.0), whose
+    // register loops keep x in LDS at no visible cost
+    const bool wsplit = wsplit_ok && ctx->tune_wsplit != 2 && (ctx->tune_wsplit == 1 || t == CIMA_GGML_Q6_K);
+    if (wsplit) {
+        p.rows = 1;
+        p.iters = wq <= 64 ? 1 : 2;
+        p.lpr_shift = 6;
+        p.ring = p.ringl = false;
+        p.grid = (unsigned)n * (unsigned)(kGemvThreads / 64);  // row groups: one row per workgroup
+    }
     if (dma)
         snprintf(name, sizeof name, "cima_gemv_%s_l%d_i%d_%s_dma%d%s%s", F->name, 1 << p.lpr_shift, p.iters,
                  act == CIMA_DT_F32 ? "f32" : "f16", depth, kind_sfx, epi ? "_epi" : "");
+    else if (wsplit)
+        snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d_%s_ksplit%s", F->name, p.iters,
+                 act == CIMA_DT_F32 ? "f32" : "f16", epi ? "_epi" : "");
     else
         snprintf(name, sizeof name, "cima_gemv_%s_r%d_i%d_%s%s%s%s", F->name, p.rows, p.iters,
                  act == CIMA_DT_F32 ? "f32" : "f16", p.ring ? "_ring" : (p.ringl ? "_ringl" : ""), kind_sfx,
@@ -391,7 +419,8 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     // persistent grid: one workgroup per CU for the item ring and for Q8_0,
     // two otherwise (measured on MI355X)
     const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs
-                                       : (dma ? dma_wgs : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2));
+                                       : (dma ? dma_wgs
+                                              : (wsplit ? 2 : ((p.ring || p.ringl || t == CIMA_GGML_Q8_0) ? 1 : 2)));
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;
@@ -496,11 +525,18 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
                 for (const char* dk : {"f32_dma%d", "f32_dma%d_epi", "f32_dma%d_pair", "f32_dma%d_pair_epi", "f16_dma%d",
                                        "f16_dma%d_epi", "f16_dma%d_pair", "f16_dma%d_pair_epi", "f16_dma%d_att_epi",
                                        "f16_dma%d_amax"}) {
+                    if (!dma_built(li[0], li[1], dd, strstr(dk, "pair") != nullptr)) continue;
                     char sfx[48], name[96];
                     snprintf(sfx, sizeof sfx, dk, dd);
                     snprintf(name, sizeof name, "cima_gemv_%s_l%d_i%d_%s", F->name, li[0], li[1], sfx);
                     if (!rc) rc = add(F->gemv_module, name);
                 }
+        for (int it = 1; it <= 2; it++)
+            for (const char* rk : {"_f32_ksplit", "_f32_ksplit_epi", "_f16_ksplit", "_f16_ksplit_epi"}) {
+                char name[96];
+                snprintf(name, sizeof name, "cima_gemv_%s_r1_i%d%s", F->name, it, rk);
+                if (!rc) rc = add(F->gemv_module, name);
+            }
         for (const char* rk : {"_f32_ringl", "_f32_ringl_epi", "_f16_ringl", "_f16_ringl_epi"}) {
             char name[96];
             snprintf(name, sizeof name, "cima_gemv_%s_r1_i1%s", F->name, rk);
@@ -578,6 +614,7 @@ int cima_hip_init(int device, const char* code_dir, cima_hip_ctx** out) {
     if (const char* s = getenv("CIMA_GEMV_DMA")) ctx->tune_dma = atoi(s);
     if (const char* s = getenv("CIMA_GEMM_XCHECK")) ctx->gemm_xcheck = atoi(s) != 0;
     if (const char* s = getenv("CIMA_GEMM_KSPLIT")) ctx->tune_ksplit = atoi(s);
+    if (const char* s = getenv("CIMA_GEMV_WSPLIT")) ctx->tune_wsplit = atoi(s);
     if (er || el) {
         if (int r = cima_hip_set_gemv_tuning(ctx, er, el)) {
             cima_hip_destroy(ctx);
@@ -675,6 +712,13 @@ int cima_hip_gemm_status(cima_hip_ctx* ctx, unsigned int* flags, int clear) {
         if ((e = hipMemcpy(ctx->gemm_status, &zero, sizeof zero, hipMemcpyHostToDevice)) != hipSuccess)
             return hip_fail(e, api);
     }
+    return 0;
+}
+
+int cima_hip_set_gemv_wsplit(cima_hip_ctx* ctx, int mode) {
+    if (!ctx) return fail(CIMA_E_NOT_INIT, "cima_hip_set_gemv_wsplit: null context");
+    if (mode < 0 || mode > 2) return fail(CIMA_E_INVALID, "cima_hip_set_gemv_wsplit: mode %d is not 0, 1 or 2", mode);
+    ctx->tune_wsplit = mode;
     return 0;
 }
 

@@ -898,7 +898,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 
     // x chunks per thread for the longest row this variant serves (ITERS
     // units of 64 lanes; 8 for the stepped item ring): k / 16 / GNT
-    constexpr int XB = RING == 3 ? 2 : ((RING == 2 ? 8 : ITERS) * F::UE * 4 + GNT - 1) / GNT;
+    constexpr int XB = RING >= 3 ? 2 : ((RING == 2 ? 8 : ITERS) * F::UE * 4 + GNT - 1) / GNT;
     // x -> LDS; the caller has the first weights in flight (and, for plain
     // x, x's first batch ahead of them in `xb`)
     auto stage = [&](XBatch<ACT, XB>& xb) {
@@ -909,7 +909,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             xa.load(xt, k >> 4);
             if constexpr (RING == 3) stage_x_loop<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
             else stage_x<ACT_F32, XB, F::PADSH>(xt, k, xa, xq, xs, xsum, nullptr, 0.f);
-        } else if constexpr (RING == 3) {
+        } else if constexpr (RING >= 3) {
             stage_x_loop<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
         } else {
             stage_x<ACT, XB, F::PADSH>(x, k, xb, xq, xs, xsum, ext.norm_w, ext.eps);
@@ -1114,6 +1114,109 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
 #pragma unroll
         for (int b = 0; b < DEPTH; b++)
             if (base + b < items) consume(ring[b]);
+    } else if constexpr (RING == 4) {
+        // k split over the waves of the workgroup, for long rows: the
+        // workgroup takes rows blockIdx.x, blockIdx.x + gridDim.x, ...; wave
+        // w takes the w-th quarter of every row's units (lane l: units
+        // w UQ + l + 64 j, j < ITERS), so each lane's x fragment is fixed
+        // for the whole kernel and held in registers, and the four waves
+        // stream four neighbouring runs of the same row.  Each wave's
+        // partial sum goes to LDS; after every KB rows (one barrier) the
+        // first KB threads add the four partials in wave order, apply the
+        // epilogue and store -- the partials are double-buffered, so one
+        // barrier per batch suffices.  Weights come through an item ring of
+        // DEPTH rows as in RING 1.  The epilogue operands of the
+        // workgroup's first 64 rows are loaded with x, one per lane.
+        static_assert(R == 1 && !PAIR && !AMAX && XS == 0, "k-split rows serve plain and epilogue GEMVs");
+        constexpr int DEPTH = CIMA_RING_DEPTH;
+        constexpr int KB = 16;  // rows per batch
+        const int UQ = (U + GNW - 1) / GNW;
+        const int u0 = wave * UQ, u1 = min(u0 + UQ, U);
+        int qu[ITERS];
+        bool qok[ITERS];
+#pragma unroll
+        for (int j = 0; j < ITERS; j++) {
+            const int u = u0 + lane + 64 * j;
+            qok[j] = u < u1;
+            qu[j] = min(u, U - 1);
+        }
+        const int nrow = (int)blockIdx.x < n ? (n - 1 - (int)blockIdx.x) / (int)gridDim.x + 1 : 0;
+        __shared__ float kred[2][KB][GNW];
+        struct Item {
+            typename F::Raw w[ITERS];
+        };
+        auto issue = [&](Item& dst, int q) {
+            const int row = min((int)blockIdx.x + q * (int)gridDim.x, n - 1);
+            const uint8_t* rp = wa + (size_t)row * row_bytes;
+#pragma unroll
+            for (int j = 0; j < ITERS; j++) dst.w[j] = F::load(rp, qu[j]);
+        };
+        constexpr int NS = DEPTH + 1;
+        Item ring[NS];
+        XBatch<ACT, XB> xb;
+        xb.load(x, k >> 4, ext.norm_w);
+        float ep1 = 0.f, ep2 = 0.f;
+        auto epi_load = [&](int b) {  // rows q = 64 b + lane
+            const int row = min((int)blockIdx.x + (64 * b + lane) * (int)gridDim.x, n - 1);
+            ep1 = load_act<ACT>(p1, has1 ? row : 0);
+            ep2 = load_act<ACT>(p2, has2 ? row : 0);
+        };
+        if constexpr (EPI) epi_load(0);
+#pragma unroll
+        for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
+        __builtin_amdgcn_sched_barrier(0);
+        stage(xb);
+        typename F::Xf xr[ITERS];
+#pragma unroll
+        for (int j = 0; j < ITERS; j++) F::loadx(xq, xs, xsum, qu[j], xr[j]);
+        // rows [KB bt, KB bt + KB) of batch bt: sum, epilogue, store
+        auto finalize = [&](int bt) {
+            const int q0 = KB * bt;
+            if constexpr (EPI) {
+                if ((q0 & 63) == 0 && q0 > 0 && wave == 0) epi_load(q0 >> 6);
+            }
+            float e1 = 0.f, e2 = 0.f;
+            if constexpr (EPI) {
+                e1 = __shfl(ep1, (q0 + lane) & 63);
+                e2 = __shfl(ep2, (q0 + lane) & 63);
+            }
+            const int q = q0 + (int)threadIdx.x;
+            if (wave == 0 && threadIdx.x < KB && q < nrow) {
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < GNW; w++) v += kred[bt & 1][threadIdx.x][w];
+                if constexpr (EPI) {
+                    if (has1) v += e1;
+                    if (has2) v += e2;
+                }
+                const int row = (int)blockIdx.x + q * (int)gridDim.x;
+                if constexpr (ACT == ACT_F32) static_cast<float*>(y)[row] = v;
+                else static_cast<uint16_t*>(y)[row] = (uint16_t)f2h(v);
+            }
+        };
+        auto compute = [&](const Item& it, int q) {
+            float p = 0.f;
+#pragma unroll
+            for (int j = 0; j < ITERS; j++) p += qok[j] ? wdot(it.w[j], xr[j], qu[j]) : 0.f;
+            p = group_sum_last(p, 64);
+            if (lane == 63) kred[(q / KB) & 1][q % KB][wave] = p;
+            if (q % KB == KB - 1 || q == nrow - 1) {
+                __syncthreads();
+                finalize(q / KB);
+            }
+        };
+        int base = 0;
+        for (; base + NS <= nrow; base += NS) {
+#pragma unroll
+            for (int b = 0; b < NS; b++) {
+                issue(ring[(b + DEPTH) % NS], base + b + DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
+                compute(ring[b], base + b);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < DEPTH; b++)
+            if (base + b < nrow) compute(ring[b], base + b);
     } else if constexpr (RING == 3) {
         // Direct-to-LDS row streaming.  An item is one segment of SEGU =
         // LPR * ITERS consecutive units of each of the wave's GPW rows (one
@@ -1441,15 +1544,33 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
     GEMV_DMA_ACT(FN, F, L, LS, IT, ACT_F32, f32, D) GEMV_DMA_ACT(FN, F, L, LS, IT, ACT_F16, f16, D)             \
     GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma##D##_att_epi, F, IT, ACT_F16, 0, 1, 1, 0, LS, D)      \
     GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma##D##_amax, F, IT, ACT_F16, 0, 0, 0, 1, LS, D)
-#define GEMV_DMA_SHAPE(FN, F, L, LS, IT) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 1) GEMV_DMA_SHAPE_D(FN, F, L, LS, IT, 2)
+// two items in flight: built for the gate+up pair at every shape and for
+// the short-row shapes (16 and 32 lanes, one unit), the cases the host
+// picks them for
+#define GEMV_DMA_PAIR2(FN, F, L, LS, IT)                                                                       \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f32_dma2_pair, F, IT, ACT_F32, 1, 0, 0, 0, LS, 2)             \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f32_dma2_pair_epi, F, IT, ACT_F32, 1, 1, 0, 0, LS, 2)         \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma2_pair, F, IT, ACT_F16, 1, 0, 0, 0, LS, 2)             \
+    GEMV_KERNEL_D(cima_gemv_##FN##_l##L##_i##IT##_f16_dma2_pair_epi, F, IT, ACT_F16, 1, 1, 0, 0, LS, 2)
+// k split over the waves (long rows): cima_gemv_<fmt>_r1_i<1|2>_<f32|f16>_ksplit[_epi]
+#define GEMV_KSPLIT_IT(FN, F, IT)                                                                      \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ksplit, F, 1, IT, ACT_F32, 0, 0, 0, 0, 4)               \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f32_ksplit_epi, F, 1, IT, ACT_F32, 0, 1, 0, 0, 4)           \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ksplit, F, 1, IT, ACT_F16, 0, 0, 0, 0, 4)               \
+    GEMV_KERNEL(cima_gemv_##FN##_r1_i##IT##_f16_ksplit_epi, F, 1, IT, ACT_F16, 0, 1, 0, 0, 4)
+#define GEMV_KSPLIT(FN, F) GEMV_KSPLIT_IT(FN, F, 1) GEMV_KSPLIT_IT(FN, F, 2)
+
 #define GEMV_DMA(FN, F)                                                                                 \
-    GEMV_DMA_SHAPE(FN, F, 64, 6, 1) GEMV_DMA_SHAPE(FN, F, 64, 6, 2) GEMV_DMA_SHAPE(FN, F, 32, 5, 1)       \
-    GEMV_DMA_SHAPE(FN, F, 32, 5, 2) GEMV_DMA_SHAPE(FN, F, 16, 4, 1)
+    GEMV_DMA_SHAPE_D(FN, F, 64, 6, 1, 1) GEMV_DMA_SHAPE_D(FN, F, 64, 6, 2, 1) GEMV_DMA_SHAPE_D(FN, F, 32, 5, 1, 1) \
+    GEMV_DMA_SHAPE_D(FN, F, 32, 5, 2, 1) GEMV_DMA_SHAPE_D(FN, F, 16, 4, 1, 1)                          \
+    GEMV_DMA_SHAPE_D(FN, F, 32, 5, 1, 2) GEMV_DMA_SHAPE_D(FN, F, 16, 4, 1, 2)                          \
+    GEMV_DMA_PAIR2(FN, F, 64, 6, 1) GEMV_DMA_PAIR2(FN, F, 64, 6, 2) GEMV_DMA_PAIR2(FN, F, 32, 5, 2)
 
 // (rows, unit steps) shapes: R * ITERS <= 8, R <= 2
 #define GEMV_FMT(FN, F)                                                                         \
     GEMV_ACT(FN, F, 1, 1) GEMV_ACT(FN, F, 1, 2) GEMV_ACT(FN, F, 1, 4) GEMV_ACT(FN, F, 1, 8)   \
-    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F) GEMV_DMA(FN, F)
+    GEMV_ACT(FN, F, 2, 1) GEMV_ACT(FN, F, 2, 2) GEMV_ACT(FN, F, 2, 4) GEMV_RING(FN, F) GEMV_DMA(FN, F) \
+    GEMV_KSPLIT(FN, F)
 
 // the formats of this code object: the file is compiled once per set (in
 // parallel), each set to its own code object

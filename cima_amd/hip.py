@@ -34,7 +34,7 @@ EXPORTS = (
     "cima_hip_init", "cima_hip_destroy", "cima_hip_bind", "cima_hip_set_stream", "cima_hip_use_own_stream",
     "cima_hip_get_stream",
     "cima_hip_sync", "cima_hip_last_error", "cima_hip_is_fatal", "cima_hip_num_cu", "cima_hip_set_gemv_tuning",
-    "cima_hip_set_gemv_dma", "cima_hip_set_gemv_grid", "cima_hip_gemm_status", "cima_hip_set_gemm_tile",
+    "cima_hip_set_gemv_dma", "cima_hip_set_gemv_wsplit", "cima_hip_set_gemv_grid", "cima_hip_gemm_status", "cima_hip_set_gemm_tile",
     "cima_hip_gguf_gemv", "cima_hip_rmsnorm_gguf_gemv",
     "cima_hip_gguf_gemv_swiglu", "cima_hip_gguf_gemm", "cima_hip_gguf_gemm_slab", "cima_hip_gguf_dequant", "cima_hip_gguf_gather",
     "cima_hip_rmsnorm", "cima_hip_rope", "cima_hip_kv_append", "cima_hip_attn_decode_split", "cima_hip_attn_reduce",
@@ -103,6 +103,7 @@ def load_library(path: str = LIBHIP) -> ctypes.CDLL:
     L.cima_hip_num_cu.argtypes = [P]
     L.cima_hip_set_gemv_tuning.argtypes = [P, I, I]
     L.cima_hip_set_gemv_dma.argtypes = [P, I]
+    L.cima_hip_set_gemv_wsplit.argtypes = [P, I]
     L.cima_hip_gemm_status.argtypes = [P, ctypes.POINTER(ctypes.c_uint), I]
     L.cima_hip_set_gemv_grid.argtypes = [P, I]
     L.cima_hip_set_gemm_tile.argtypes = [P, I]
@@ -230,6 +231,10 @@ class HipCtx:
     def set_gemv_dma(self, mode: int = 0) -> None:
         """GEMV main loop: 0 = heuristic, 1 = direct-to-LDS streaming where built, 2 = register loops."""
         self._check(self.lib.cima_hip_set_gemv_dma(self.handle, int(mode)))
+
+    def set_gemv_wsplit(self, mode: int = 0) -> None:
+        """GEMV rows split over the workgroup's waves: 0 = heuristic, 1 = wherever it applies, 2 = never."""
+        self._check(self.lib.cima_hip_set_gemv_wsplit(self.handle, int(mode)))
 
     def gemm_status(self, clear: bool = True) -> int:
         """X range flags of the prefill GEMMs since the last clear (waits for the

@@ -101,12 +101,22 @@ int cima_hip_set_gemv_tuning(cima_hip_ctx* ctx, int rows, int lanes_per_row);
 
 /* GEMV main-loop choice (no counterpart in the reference): 0 = built-in
  * heuristic, 1 = the direct-to-LDS streaming kernels with one item in flight
- * per wave wherever they are built and fit, 3 = the same with two, 2 =
- * never them (the register-ring kernels).  Environment variable
+ * per wave wherever they are built and fit, 3 = the same with two where
+ * built (the gate+up pair, rows of one unit at 16 or 32 lanes; else one),
+ * 2 = never them (the register-ring kernels).  Environment variable
  * CIMA_GEMV_DMA at init.  A set_gemv_tuning override of rows selects the
  * register kernels; one of lanes does too under the heuristic (mode 0) and
  * picks the streaming kernels' lanes per row (16, 32 or 64) under 1 or 3. */
 int cima_hip_set_gemv_dma(cima_hip_ctx* ctx, int mode);
+
+/* GEMV rows split over the workgroup's four waves (no counterpart in the
+ * reference): for rows of more than 128 units (k > 8192 at Q4_K, k > 4096
+ * at Q8_0) each wave takes a quarter of every row with its x fragment in
+ * registers, and the four partial sums add in a fixed order.  0 = built-in
+ * heuristic (Q6_K), 1 = wherever it applies (plain and epilogue GEMVs,
+ * rows of at most 512 units), 2 = never.  Environment variable
+ * CIMA_GEMV_WSPLIT at init. */
+int cima_hip_set_gemv_wsplit(cima_hip_ctx* ctx, int mode);
 
 /* GEMV grid tuning (no counterpart in the reference): the persistent grid
  * holds at most this many 256-thread workgroups per CU (0 = the default of 1, or fewer
