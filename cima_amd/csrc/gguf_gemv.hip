@@ -1473,7 +1473,12 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             unsigned long long m = 0ull;
 #pragma unroll
             for (int w = 0; w < GNW; w++) m = umax64(m, red[w]);
-            atomicMax(ext.slot, m);
+            // every workgroup's atomic lands on one word: skip it where the
+            // slot already holds a larger key (the slot only grows, so a
+            // stale read can only let through an atomic that was not
+            // needed, never skip one that was)
+            const unsigned long long cur = __hip_atomic_load(ext.slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (m > cur) atomicMax(ext.slot, m);
         }
     }
 }
