@@ -377,9 +377,19 @@ constexpr int GNW = CIMA_GEMV_WAVES;
 constexpr int GNT = 64 * GNW;
 
 // Item-ring depth: row groups in flight per lane for items of one unit of
-// one weight stream, and for items of two (two units, or the gate|up pair)
+// one weight stream, and for items of two (two units, or the gate|up pair).
+// The one-unit item ring (RING 1) keeps three: measured on MI355X, cold,
+// one workgroup per CU, depth 4 -> 3: Q4_K 14336x4096 8.21 -> 7.96 us,
+// 4096x4096 5.04 -> 4.61, 6144x4096 5.60 -> 5.27, Q5_K 14336x4096 10.12 ->
+// 9.19, Q6_K 11.82 -> 10.78 (2: 10.41), IQ4_XS 10.79 -> 9.83; the Q6_K
+// head unchanged.  More bytes in flight per CU only queue behind HBM and
+// leave more items to compute after the last one lands.  The stepped ring
+// and the wave k-split keep four.
 #ifndef CIMA_RING_DEPTH
 #define CIMA_RING_DEPTH 4
+#endif
+#ifndef CIMA_RING_DEPTH_ITEM
+#define CIMA_RING_DEPTH_ITEM 3
 #endif
 #ifndef CIMA_RING_DEPTH_PAIR
 #define CIMA_RING_DEPTH_PAIR 2
@@ -976,7 +986,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         // unrolled over the slots so slot indices are compile-time constants.  Items past the lane's last
         // row group re-load that row group (a cache hit) and write nothing.
         static_assert(ITERS <= 2 && R == 1, "the item ring serves one-row groups of one or two units");
-        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
+        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH_ITEM;
         struct Item {
             typename F::Raw w[S][ITERS];
             float e1[R], e2[R];
