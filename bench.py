@@ -61,9 +61,10 @@ def parse():
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--calib", action="store_true",
                     help="also run a 256 MiB device copy (calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--leg", choices=["q8_0_14336x4096", "q8_0_pair", "q8_0_head_151936x896"], default=None,
-                    help="run only this GEMV --steps times on cycled cold copies (and --calib), for counter "
-                         "passes of rocprofv3; prints nothing")
+    ap.add_argument("--leg", choices=["q8_0_14336x4096", "q8_0_pair", "q8_0_head_151936x896", "q4_k_14336x4096",
+                                        "q4_k_4096x14336", "q4_k_gemm_m16", "q4_k_gemm_m128", "q4_k_gemm_m512"], default=None,
+                    help="run only this GEMV or prefill GEMM --steps times on cycled cold copies (and --calib), "
+                         "for counter passes of rocprofv3; prints nothing")
     return ap.parse_args()
 
 
@@ -82,8 +83,7 @@ def main():
 
     import cima_amd.build as cbuild
 
-    if not cbuild.built():
-        cbuild.build()
+    cbuild.ensure()
     import torch
     from cima_amd import nf4, synth
     from cima_amd.hip import HipCtx
@@ -152,11 +152,25 @@ def main():
         del src, dst
     if args.leg:
         # one GEMV shape alone, for per-dispatch counters (FETCH_SIZE /
-        # WRITE_SIZE): Q8_0 at Llama-3-8B gate/up, the Q8_0 gate+up pair,
-        # or the Qwen2.5-0.5B Q8_0 tied head with its argmax (f16 x)
-        n, k = (151936, 896) if args.leg == "q8_0_head_151936x896" else (FFN, HID)
+        # WRITE_SIZE): Q8_0 or Q4_K at Llama-3-8B gate/up, Q4_K down, the
+        # Q8_0 gate+up pair, or the Qwen2.5-0.5B Q8_0 tied head with its
+        # argmax (f16 x)
+        if args.leg.startswith("q4_k_gemm_m"):
+            # config 4's prefill dequant-GEMM at one token count (X bf16, Y fp32)
+            m = int(args.leg[len("q4_k_gemm_m"):])
+            gbufs = [torch.from_numpy(synth.weights(Q4_K, 300, 0.02, FFN, HID)).to(dev)]
+            gbufs += [gbufs[0].clone() for _ in range(11)]
+            gslab = torch.empty(32 << 20, dtype=torch.uint8, device=dev)
+            gx = torch.from_numpy(synth.normal(301, 1.0, m * HID)).to(dev).to(torch.bfloat16).reshape(m, HID)
+            gy = torch.empty((m, FFN), device=dev)
+            for i in range(args.steps):
+                ctx.gguf_gemm_slab(Q4_K, gx, gbufs[i % len(gbufs)], gy, m, FFN, HID, gslab)
+            torch.cuda.synchronize()
+            return
+        n, k = {"q8_0_head_151936x896": (151936, 896), "q4_k_4096x14336": (HID, FFN)}.get(args.leg, (FFN, HID))
         pair = args.leg == "q8_0_pair"
-        copies = [torch.from_numpy(synth.weights(Q8_0, 400 + i, 0.02, n, k)).to(dev) for i in range(2 if pair else 1)]
+        t = Q4_K if args.leg.startswith("q4_k") else Q8_0
+        copies = [torch.from_numpy(synth.weights(t, 400 + i, 0.02, n, k)).to(dev) for i in range(2 if pair else 1)]
         copies = [c.clone() for c in copies for _ in range(6)]
         if args.leg == "q8_0_head_151936x896":
             xs = torch.from_numpy(synth.normal(9, 1.0, k)).to(dev).half()
@@ -172,7 +186,7 @@ def main():
             elif args.leg == "q8_0_head_151936x896":
                 ctx.gguf_gemv_argmax(Q8_0, xs, None, 0.0, copies[i % len(copies)], ys, n, k, slot)
             else:
-                ctx.gguf_gemv(Q8_0, xs, copies[i % len(copies)], None, ys, n, k, 0)
+                ctx.gguf_gemv(t, xs, copies[i % len(copies)], None, ys, n, k, 0)
         torch.cuda.synchronize()
         return
 

@@ -77,8 +77,10 @@ def source_hash() -> str:
                 h.update(name.encode())
                 with open(path, "rb") as f:
                     h.update(f.read())
+    # the commands with the checkout's own path taken out, so a copy of the
+    # tree at another path (a GPU host's scratch directory) hashes the same
     for cmd in _cmds().values():
-        h.update(" ".join(cmd).encode())
+        h.update(" ".join(cmd).replace(ROOT, "<root>").encode())
     return h.hexdigest()
 
 
@@ -107,12 +109,27 @@ def build(verbose: bool = False) -> None:
 
 
 def built() -> bool:
-    """True when every artefact exists and was built from the sources as
-    they are now (the stamp written by build() matches source_hash())."""
-    if not all(os.path.exists(p) for p in (*HSACOS.values(), LIBHIP, LIBSYNTH, STAMP)):
+    """True when every artefact exists (whether or not it is current)."""
+    return all(os.path.exists(p) for p in (*HSACOS.values(), LIBHIP, LIBSYNTH))
+
+
+def current() -> bool:
+    """True when the artefacts were built from the sources as they are now
+    (the stamp written by build() matches source_hash())."""
+    if not (built() and os.path.exists(STAMP)):
         return False
     with open(STAMP) as f:
         return f.read().strip() == source_hash()
+
+
+def ensure() -> None:
+    """Load what is built: compile only when an artefact is missing, and warn
+    (without rebuilding) when the sources changed since the last build."""
+    if not built():
+        build()
+    elif not current():
+        print("cima_amd: the native artefacts predate the sources under csrc/ or include/; "
+              "run python -m cima_amd.build to rebuild them", file=sys.stderr)
 
 
 if __name__ == "__main__":

@@ -304,7 +304,6 @@ class HipCtx:
                                                      int(slab_bytes)))
 
     @staticmethod
-    @staticmethod
     def nf4_slab_bytes(m: int, n: int, k: int, x_f16: bool = False) -> int:
         """Slab size with which ``nf4_gemm_slab``'s slab route decodes W in
         one slice (W as f16); the fused route needs none.  ``m`` and

@@ -28,8 +28,7 @@ def _ensure_built():
     import cima_amd.build as b
     import oracle
 
-    if not b.built():
-        b.build()
+    b.ensure()
     oracle.build()
 
 
