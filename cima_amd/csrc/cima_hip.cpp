@@ -416,12 +416,14 @@ int gemv_common(cima_hip_ctx* ctx, int t, const void* x, const void* wa, const v
     hipError_t oe = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&resident, f, threads, p.lds);
     if (oe != hipSuccess) return hip_fail(oe, "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
     if (resident < 1) resident = 1;
-    // persistent grid: one workgroup per CU for the item rings, the wave
-    // split and Q8_0, two otherwise (measured on MI355X; the wave split of
-    // Q6_K 4096x14336, cold: 14.5 us at two workgroups per CU, 13.5 at one)
+    // persistent grid: one workgroup per CU for the item ring, the wave
+    // split and Q8_0's other loops, two otherwise, the stepped ring included
+    // (measured on MI355X; the wave split of Q6_K 4096x14336, cold: 14.5 us
+    // at two workgroups per CU, 13.5 at one)
     const int want = ctx->tune_wgs > 0 ? ctx->tune_wgs
                                        : (dma ? dma_wgs
-                                              : ((p.ring || p.ringl || wsplit || t == CIMA_GGML_Q8_0) ? 1 : 2));
+                                              : (p.ringl ? 2
+                                                         : ((p.ring || wsplit || t == CIMA_GGML_Q8_0) ? 1 : 2)));
     if (want < resident) resident = want;
     unsigned cap = (unsigned)(resident * ctx->num_cu);
     if (p.grid > cap) p.grid = cap;

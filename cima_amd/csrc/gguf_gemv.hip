@@ -384,9 +384,15 @@ constexpr int GNT = 64 * GNW;
 // 9.19, Q6_K 11.82 -> 10.78 (2: 10.41), IQ4_XS 10.79 -> 9.83; the Q6_K
 // head unchanged.  More bytes in flight per CU only queue behind HBM and
 // leave more items to compute after the last one lands.  The stepped ring
-// and the wave k-split keep four.
+// keeps three (at two workgroups per CU, measured on MI355X, 4096x14336,
+// cold, against four at one: Q8_0 17.05 -> 16.72 us, Q4_0 11.45 -> 11.07,
+// Q4_1 10.74 -> 10.26, Q5_0 12.89 -> 12.40, Q5_1 12.02 -> 11.49); the wave
+// k-split keeps four.
 #ifndef CIMA_RING_DEPTH
 #define CIMA_RING_DEPTH 4
+#endif
+#ifndef CIMA_RING_DEPTH_STEP
+#define CIMA_RING_DEPTH_STEP 3
 #endif
 #ifndef CIMA_RING_DEPTH_ITEM
 #define CIMA_RING_DEPTH_ITEM 3
@@ -1052,7 +1058,7 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         // of a row group reduces and writes it.  Items past the lane's last
         // row group re-load it and write nothing.
         static_assert(ITERS <= 2 && R == 1, "the stepped item ring serves one-row groups");
-        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH;
+        constexpr int DEPTH = S * ITERS >= 2 ? CIMA_RING_DEPTH_PAIR : CIMA_RING_DEPTH_STEP;
         const int T = (U + (ITERS << lpr_shift) - 1) / (ITERS << lpr_shift);
         int items = 0;  // per * T, once the counts are known
         struct Item {
