@@ -400,6 +400,15 @@ constexpr int GNT = 64 * GNW;
 #ifndef CIMA_RING_DEPTH_PAIR
 #define CIMA_RING_DEPTH_PAIR 2
 #endif
+// Extra items of the item ring's first issue, in flight while x is fetched
+// and staged (see RING 1).  Measured on MI355X, cold, bit-identical
+// results, one extra against none: Q4_K 14336x4096 7.99 -> 7.80 us,
+// 4096x4096 4.58 -> 4.39, 6144x4096 5.28 -> 5.06, Q8_0 4096x4096 6.51 ->
+// 6.24, the Q4_K gate+up pair and Q6_K unchanged; two or three extra were
+// slower than none (Q4_K 14336x4096 8.25 / 8.39).
+#ifndef CIMA_RING_BURST
+#define CIMA_RING_BURST 1
+#endif
 
 // sum over the workgroup (every thread calls it; all get the total)
 DEV float block_sum(float v) {
@@ -1013,13 +1022,17 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
         };
         // DEPTH + 1 slots: item q + DEPTH is issued into the slot freed by
         // item q - 1 before item q is computed, so DEPTH items stay in flight
-        // while a wave computes (issuing after the compute left DEPTH - 1)
-        constexpr int NS = DEPTH + 1;
+        // while a wave computes (issuing after the compute left DEPTH - 1).
+        // With BURST > 0, BURST more items go out with the first ones (while
+        // x is fetched and staged) and the first BURST items are computed
+        // without issuing, after which DEPTH stay in flight as before.
+        constexpr int BURST = CIMA_RING_BURST;
+        constexpr int NS = DEPTH + 1 + BURST;
         Item ring[NS];
         XBatch<ACT, XB> xb;
         if constexpr (XS == 0) xb.load(x, k >> 4, ext.norm_w);
 #pragma unroll
-        for (int d = 0; d < DEPTH; d++) issue(ring[d], d);
+        for (int d = 0; d < DEPTH + BURST; d++) issue(ring[d], d);
         __builtin_amdgcn_sched_barrier(0);
         counts();
         stage(xb);
@@ -1036,21 +1049,36 @@ __device__ void gemv_body(const void* __restrict__ x, const uint8_t* __restrict_
             }
             finish(acc, it.e1, it.e2, q);
         };
+        // the burst's first items (a padding item past the wave's count
+        // computes a re-loaded row and writes nothing)
+#pragma unroll
+        for (int b = 0; b < BURST; b++) compute(ring[b], b);
         // whole rounds of NS items with no condition in the body, then the
-        // wave's remaining items (all in flight already; no padding item is
-        // waited for)
-        int base = 0;
+        // wave's remaining items
+        int base = BURST;
         for (; base + NS <= per; base += NS) {
 #pragma unroll
             for (int b = 0; b < NS; b++) {
-                issue(ring[(b + DEPTH) % NS], base + b + DEPTH);
+                issue(ring[(BURST + b + DEPTH) % NS], base + b + DEPTH);
                 __builtin_amdgcn_sched_barrier(0);
-                compute(ring[b], base + b);
+                compute(ring[(BURST + b) % NS], base + b);
             }
         }
+        if constexpr (BURST == 0) {
+            // all in flight already; no padding item is waited for
 #pragma unroll
-        for (int b = 0; b < DEPTH; b++)
-            if (base + b < per) compute(ring[b], base + b);
+            for (int b = 0; b < DEPTH; b++)
+                if (base + b < per) compute(ring[b], base + b);
+        } else {
+            // up to NS - 1 items remain, not all issued yet: issue ahead as
+            // in the rounds (padding items past the count re-load a row)
+#pragma unroll
+            for (int b = 0; b < NS - 1; b++) {
+                issue(ring[(BURST + b + DEPTH) % NS], base + b + DEPTH);
+                __builtin_amdgcn_sched_barrier(0);
+                if (base + b < per) compute(ring[(BURST + b) % NS], base + b);
+            }
+        }
     } else if constexpr (RING == 2) {
         // Stepped item ring (long rows): a row group takes T steps of ITERS
         // units per lane, and an item is one step of one row group -- the
