@@ -514,6 +514,63 @@ def test_item_ring_matches_double_buffer(t):
         c.close()
 
 
+@pytest.mark.parametrize("t", FORMATS, ids=[NAMES[t] for t in FORMATS])
+def test_streaming_matches_register_loops(t):
+    """The direct-to-LDS streaming kernels (the _dma<D> family, forced on
+    with CIMA_GEMV_DMA=1 for one item in flight and 3 for two) against the
+    register loops (forced off with CIMA_GEMV_DMA=2): the same product up
+    to the order of the k sum (1e-6 with fp32 y, one f16 rounding with f16
+    y) for plain, residual + bias and gate+up pair GEMVs, ragged row
+    counts, rows of one and of several segments, and the argmax head's
+    index exactly."""
+    import os
+    from cima_amd.hip import HipCtx
+
+    ctxs = {}
+    for dma in ("2", "1", "3"):
+        os.environ["CIMA_GEMV_DMA"] = dma
+        try:
+            ctxs[dma] = HipCtx(0)
+        finally:
+            del os.environ["CIMA_GEMV_DMA"]
+        ctxs[dma].use_torch_stream()
+    ref_key = "2"
+    be = mg.BLOCK[t][0]
+    ue = 64 if be == 256 else 32
+    for n, k in ((37, 32 * ue), (1000, 128 * ue), (300, 300 * ue)):
+        w = torch.from_numpy(synth.weights(t, 70 + n, 0.02, n, k)).cuda()
+        wu = torch.from_numpy(synth.weights(t, 71 + n, 0.02, n, k)).cuda()
+        for dt in (torch.float32, torch.float16):
+            x = torch.from_numpy(synth.normal(72, 1.0, k)).to(dt).cuda()
+            b = torch.from_numpy(synth.normal(73, 0.1, n)).to(dt).cuda()
+            outs = {}
+            for key, c in ctxs.items():
+                y0 = torch.empty(n, dtype=dt, device="cuda")
+                c.gguf_gemv(t, x, w, None, y0, n, k, 0)
+                y1 = torch.from_numpy(synth.normal(74, 1.0, n)).to(dt).cuda()
+                c.gguf_gemv(t, x, w, b, y1, n, k, 1)
+                y2 = torch.empty(n, dtype=dt, device="cuda")
+                c.gguf_gemv_swiglu(t, x, w, wu, b, b, y2, n, k)
+                outs[key] = [host(v).astype(np.float64) for v in (y0, y1, y2)]
+            tol = 1e-6 if dt == torch.float32 else 1e-3
+            for key, o in outs.items():
+                for i in range(3):
+                    assert rel(o[i], outs[ref_key][i]) <= tol, (key, i, n, k, dt)
+        # the head: f16 x and logits, the argmax key's index
+        xh = torch.from_numpy(synth.normal(75, 1.0, k)).half().cuda()
+        idx = {}
+        for key, c in ctxs.items():
+            y = torch.empty(n, dtype=torch.float16, device="cuda")
+            slot = torch.zeros(1, dtype=torch.int64, device="cuda")
+            c.gguf_gemv_argmax(t, xh, None, 0.0, w, y, n, k, slot)
+            idx[key] = (int(host(slot)[0]) & 0xFFFFFFFF, host(y).astype(np.float64))
+        for key, (i, y) in idx.items():
+            assert rel(y, idx[ref_key][1]) <= 1e-3, (key, "argmax logits", n, k)
+            assert y[i] == y.max(), (key, "argmax index", n, k)
+    for c in ctxs.values():
+        c.close()
+
+
 def swiglu64(g, u):
     g = np.asarray(g, np.float64)
     return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
