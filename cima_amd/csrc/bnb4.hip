@@ -275,8 +275,6 @@ DEV void nf4_gemv_body(const XT* __restrict__ x, const uint8_t* __restrict__ pac
                        int n, int k, int bshift) {
     extern __shared__ uint4 smem_[];
     Dec dec;
-    dec.stage(reinterpret_cast<uint8_t*>(smem_), x, qmap, k, NT);
-    __syncthreads();
 
     // Work of one wave: its row groups g = wave, wave + nwaves, ..., each
     // walked in T steps of 64 segments (one per lane).  An item is one step
@@ -291,15 +289,18 @@ DEV void nf4_gemv_body(const XT* __restrict__ x, const uint8_t* __restrict__ pac
     const int groups = (n + R - 1) / R;
     const int nwaves = gridDim.x * WPG;
     const int wave = blockIdx.x * WPG + (threadIdx.x >> 6);
-    if (wave >= groups) return;
-    const int items = ((groups - 1 - wave) / nwaves + 1) * T;
+    // a wave past the last row group loads the last one's rows (its loads
+    // are never used) rather than branching around the loads, so the first
+    // items can go out before x and the table are staged
+    const int wv = min(wave, groups - 1);
+    const int items = ((groups - 1 - wv) / nwaves + 1) * T;
     const size_t rowb = (size_t)(k >> 1);
 
     struct Item {
         uint4 w[R];
         float a[R];
     };
-    int ig = wave, it = 0;  // next item to load: group, step
+    int ig = wv, it = 0;  // next item to load: group, step
     auto issue = [&](Item& s) {
         const int j = min(it * 64 + lane, segs - 1);
 #pragma unroll
@@ -316,7 +317,7 @@ DEV void nf4_gemv_body(const XT* __restrict__ x, const uint8_t* __restrict__ pac
     // finished rows wait in lane `slot` of res / rowv and are written once
     // after the loop, so that no store sits between the weight loads (the
     // host sizes the grid so that no wave owns more than 64 rows)
-    int cg = wave, ct = 0, slot = 0;
+    int cg = wv, ct = 0, slot = 0;
     float acc[R], res = 0.f;
     int rowv = n;
 #pragma unroll
@@ -346,8 +347,17 @@ DEV void nf4_gemv_body(const XT* __restrict__ x, const uint8_t* __restrict__ pac
     // load under a condition makes the compiler's wait counting assume the
     // worst and drain the ring.
     Item ring[D];
+    issue(ring[0]);
+    // x (and the pair table) while the first item is in flight; the rest of
+    // the ring after (measured on MI355X, cold, against issuing after the
+    // staging: 4096x4096 5.59 -> 5.03 us, 128256x4096 57.7 -> 55.6-56.3,
+    // 4096x14336 10.2-10.9 -> 10.1-10.2, 14336x4096 9.7-10.1 -> 10.25; the
+    // whole ring up front flooded HBM at 32 waves per CU: 14336x4096 11.35)
+    dec.stage(reinterpret_cast<uint8_t*>(smem_), x, qmap, k, NT);
+    __syncthreads();
+    if (wave >= groups) return;
 #pragma unroll
-    for (int d = 0; d < D; d++) issue(ring[d]);
+    for (int d = 1; d < D; d++) issue(ring[d]);
     int i = 0;
     for (; i + D <= items; i += D) {
 #pragma unroll
